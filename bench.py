@@ -1,0 +1,288 @@
+#!/usr/bin/env python
+"""MoE-layer decode benchmark (BASELINE.json metric) on one MI355X.
+
+Workload: Qwen3-30B-A3B-shaped MoE layer -- hidden
+2048, 128 experts, top-8 softmax router with renormalised weights, expert
+intermediate 768, affine 4-bit group-64 weights from N(0, 0.02); 48
+independent layer copies (16.3 GB) rotated so the 256 MB Infinity Cache
+cannot hold the working set.  Decode batch B (default 1) of bf16 N(0,1)
+tokens; synthetic, seeded data.
+
+A step = one pass of the MoE block over the batch through all 48 layer copies
+(48 layer calls).  Reported:
+  value       us per token per layer call at B (lower is better)
+  gbps        algorithmic HBM bytes per layer call / layer time
+  roofline    of the dominant kernel, timed with HIP events on its stream
+  cpu_baseline  this repo's C++/OpenMP restatement of the unpatched MLX path
+              (MLX is not installable offline) on the host cores, rank 0.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+METRIC = "MoE-layer decode µs/token + HBM GB/s (% roofline), Qwen3-30B-A3B shape 4-bit"
+HBM_PEAK_GBPS = 8000.0
+
+H, E, K, I, GS = 2048, 128, 8, 768, 64
+LAYERS = 48
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def per_expert_bytes(h=H, i=I, gs=GS) -> int:
+    """Packed gate+up+down nibbles plus bf16 scale and bias per group."""
+    gate_up = 2 * i * (h // 2 + (h // gs) * 4)
+    down = h * (i // 2 + (i // gs) * 4)
+    return gate_up + down
+
+
+def build_layers(dev, n_layers: int, seed: int = 0):
+    import torch
+
+    from zmlx_amd.layer import QuantizedMoELayer, QuantProj
+    from zmlx_amd.quant import quantize_affine
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+
+    def bank(n_out, n_in):
+        ws, ss, bs = [], [], []
+        for e0 in range(0, E, 16):
+            w = (torch.randn((16, n_out, n_in), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+            q, s, b = quantize_affine(w, GS)
+            ws.append(q), ss.append(s), bs.append(b)
+        return torch.cat(ws), torch.cat(ss), torch.cat(bs)
+
+    base = {"gate": bank(I, H), "up": bank(I, H), "down": bank(H, I)}
+    torch.cuda.synchronize()
+    layers = []
+    for li in range(n_layers):
+        copy = {k: tuple(t.clone() for t in v) for k, v in base.items()}
+        wr = (torch.randn((E, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        layers.append(QuantizedMoELayer.for_family(
+            "qwen3", wr, QuantProj(*copy["gate"]), QuantProj(*copy["up"]), QuantProj(*copy["down"]), top_k=K,
+            group_size=GS))
+    torch.cuda.synchronize()
+    return layers, base
+
+
+def capture_step(layers, x):
+    """Capture one step (every layer copy once) into a HIP graph so replays
+    measure the GPU, not Python/ctypes launch overhead."""
+    import torch
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for layer in layers:  # allocate workspaces / outputs outside capture
+            layer(x)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for layer in layers:
+            layer(x)
+    torch.cuda.synchronize()
+    return graph
+
+
+def time_layers(layers, x, steps: int, warmup: int, use_graph: bool = True) -> float:
+    """Average ms per step (one call of every layer copy)."""
+    import torch
+
+    if use_graph:
+        graph = capture_step(layers, x)
+        run = graph.replay
+    else:
+        def run():
+            for layer in layers:
+                layer(x)
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        run()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def unique_experts(layers, x):
+    import torch
+
+    counts = []
+    idxs = []
+    for layer in layers:
+        _, idx, _ = layer(x, return_routing=True)
+        idxs.append(idx)
+    torch.cuda.synchronize()
+    for idx in idxs:
+        counts.append(int(torch.unique(idx).numel()))
+    return counts, idxs
+
+
+def dominant_kernel(layers, x, idxs, steps: int):
+    """Time the fused gate/up+SwiGLU kernel alone over the rotated copies
+    (HIP events on the torch stream the kernel is launched on)."""
+    import torch
+
+    import zmlx_amd as Z
+
+    def run():
+        for layer, idx in zip(layers, idxs):
+            gate, up = layer._proj["gate"], layer._proj["up"]
+            Z.gather_qmm_swiglu(x[:, None, None, :], *gate, *up, rhs_indices=idx[:, None, :])
+
+    run()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        run()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) * 1e3 / (steps * len(layers))  # us per launch
+
+
+def cpu_baseline(base, layer0, x_host, budget_s: float = 12.0, max_tokens: int = 4096):
+    """C++/OpenMP restatement of the unpatched path on the host cores, on a
+    bounded sample of the same workload (one layer copy, single-token calls)."""
+    import numpy as np
+    import torch
+
+    from oracle import ref_lib
+
+    threads = min(len(os.sched_getaffinity(0)), 16)
+    ref_lib.lib().oref_set_threads(threads)
+
+    def bits(t):
+        return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+    def words(t):
+        return np.ascontiguousarray(t.contiguous().view(torch.int32).cpu().numpy().view(np.uint32))
+
+    banks = {k: (words(v[0]), bits(v[1]), bits(v[2])) for k, v in base.items()}
+    wr = bits(layer0._router_w)
+    x16 = bits(x_host)
+    # warm-up (page in the 340 MB layer)
+    ref_lib.moe_layer_qwen_bits(x16[:1], wr, banks["gate"], banks["up"], banks["down"], k=K)
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s and n < max_tokens:
+        ref_lib.moe_layer_qwen_bits(x16[n % x16.shape[0]:][:1], wr, banks["gate"], banks["up"], banks["down"], k=K)
+        n += 1
+    dt = time.perf_counter() - t0
+    return {
+        "value": round(dt * 1e6 / n, 2),
+        "unit": "us/token",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{n} single-token calls of one Qwen3-shaped layer copy (B=1), "
+                  f"C++/OpenMP restatement of the unpatched MLX path (MLX unavailable offline), {dt:.1f}s",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--layers", type=int, default=LAYERS)
+    ap.add_argument("--extra-batches", default="4,16")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build measures one GPU only (the decode MoE layer on one MI355X); "
+              "--gpus must be 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import zmlx_amd  # noqa: F401  (fails loudly if the HIP library is missing)
+
+    dev = torch.device("cuda:0")
+    log(f"building {args.layers} layer copies (this takes a few seconds)")
+    layers, base = build_layers(dev, args.layers)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+    batches = [args.batch] + [int(b) for b in args.extra_batches.split(",") if b and int(b) != args.batch]
+    per_b = {}
+    main_rec = None
+    for B in batches:
+        x = torch.randn((B, H), generator=gen, device=dev).to(torch.bfloat16)
+        counts, idxs = unique_experts(layers, x)
+        steps = args.steps if B == args.batch else max(5, args.steps // 4)
+        log(f"B={B}: timing {steps} steps x {len(layers)} layers")
+        ms = time_layers(layers, x, steps, args.warmup, use_graph=not args.no_graph)
+        layer_us = ms * 1e3 / len(layers)
+        avg_unique = sum(counts) / len(counts)
+        alg_bytes = avg_unique * per_expert_bytes() + E * H * 2 + 4 * B * H
+        gbps = alg_bytes / (layer_us * 1e-6) / 1e9
+        rec = {"us_per_token": round(layer_us / B, 3), "us_per_layer_call": round(layer_us, 3),
+               "gbps": round(gbps, 1), "roofline_frac": round(gbps / HBM_PEAK_GBPS, 4),
+               "unique_experts": round(avg_unique, 2), "alg_bytes_per_call": int(alg_bytes), "steps": steps,
+               "ms_per_step": round(ms, 4)}
+        per_b[str(B)] = rec
+        if B == args.batch:
+            main_rec = rec
+            kus = dominant_kernel(layers, x, idxs, max(5, steps // 2))
+            kbytes = avg_unique * 2 * I * (H // 2 + (H // GS) * 4) + B * H * 2 + B * K * I * 2
+            kgbps = kbytes / (kus * 1e-6) / 1e9
+            roof = {"bound": "hbm", "achieved": round(kgbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": round(kgbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                    "kernel": "k_gather_qmv<SWIGLU> (gate/up + SwiGLU)", "avg_launch_us": round(kus, 3),
+                    "alg_bytes_per_launch": int(kbytes)}
+        log(f"B={B}: {rec}")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("CPU baseline (C++ restatement) ...")
+        x_host = torch.randn((64, H), generator=gen, device=dev).to(torch.bfloat16)
+        cpu = cpu_baseline(base, layers[0], x_host, budget_s=args.cpu_budget)
+        log(f"CPU baseline: {cpu}")
+
+    out = {
+        "metric": METRIC,
+        "value": main_rec["us_per_token"],
+        "unit": "us/token",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": main_rec["ms_per_step"],
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "qwen3-30b-a3b-moe-layer-decode", "hidden": H, "experts": E, "top_k": K,
+                   "inter": I, "quant": "affine4-g64", "batch": args.batch, "layer_copies": len(layers),
+                   "parallelism": "none (1 GPU)"},
+        "gbps": main_rec["gbps"],
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "batches": per_b,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

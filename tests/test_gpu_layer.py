@@ -1,0 +1,232 @@
+"""GPU parity: the whole MoE block (zmoe_moe_layer) vs the oracle composition.
+
+Per stage the oracle is fed the GPU's previous-stage decision where MLX's own
+choice is unspecified (the top-k order inside a bf16 tie set), and checked:
+routing = valid top-k of the oracle's probabilities; weights within 1 bf16
+ulp; layer output within the reference tolerance (1e-2) and mostly
+bit-identical.  Configs are the BASELINE shapes at small expert counts
+(the per-expert shapes are the real ones)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import moe_oracle as O
+from tests.moe_case import bf16_randn, from_dev, make_bank, to_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def _build(dev, rng, *, H, E, I, K, mode="affine", gs=64, shared_I=0, router_std=0.02):
+    import torch
+
+    from zmlx_amd.layer import QuantProj
+
+    banks = {n: make_bank(rng, E, *(shape), mode=mode, group_size=gs)
+             for n, shape in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I)))}
+    wr = bf16_randn(rng, (E, H), router_std)
+    sh = None
+    if shared_I:
+        sh = {n: make_bank(rng, 1, *(shape), mode=mode, group_size=gs)
+              for n, shape in (("gate", (shared_I, H)), ("up", (shared_I, H)), ("down", (H, shared_I)))}
+
+    def qp(bank, squeeze=False):
+        w, s, b = bank.torch(dev)
+        if squeeze:
+            w, s = w[0], s[0]
+            b = None if b is None else b[0]
+        return QuantProj(w, s, b)
+
+    tq = {n: qp(b) for n, b in banks.items()}
+    tsh = None if sh is None else tuple(qp(sh[n], True) for n in ("gate", "up", "down"))
+    return banks, wr, sh, tq, tsh, to_bf16(wr, dev)
+
+
+def _oracle_out(x, idx, w, banks, sh, mode, gs, combine):
+    y = O.moe_experts(x, idx, banks["gate"].as_tuple(), banks["up"].as_tuple(), banks["down"].as_tuple(),
+                      group_size=gs, mode=mode)
+    out = O.moe_combine(y, w, combine)
+    out = O.bf16_round(out)
+    if sh is not None:
+        ys = O.shared_expert(x, tuple(a[0] if a is not None else None for a in sh["gate"].as_tuple()),
+                             tuple(a[0] if a is not None else None for a in sh["up"].as_tuple()),
+                             tuple(a[0] if a is not None else None for a in sh["down"].as_tuple()),
+                             group_size=gs, mode=mode)
+        out = O.bf16_round(out + ys)
+    return out
+
+
+def _cmp_out(got, ref):
+    """Reference tolerance (1e-2, test_gather_qmm_swiglu.py:84-85) and >= 90%
+    bit-identical: each output mixes K expert outputs, each of which may sit
+    one bf16 ulp from the float64 oracle (fp32 GEMV accumulation), so a few
+    percent of outputs legitimately differ in the last bit."""
+    np.testing.assert_allclose(got, ref, atol=1e-2, rtol=1e-2)
+    ulp = O.bf16_ulp_diff(got, ref)
+    assert (ulp == 0).mean() >= 0.90, f"exact fraction {(ulp == 0).mean():.4f}"
+
+
+@pytest.mark.parametrize("B", [1, 4, 16])
+def test_layer_qwen3_shape(dev, B):
+    """Qwen3-30B-A3B per-expert shapes (H 2048, I 768, top-8), 32 experts."""
+    import torch
+
+    from zmlx_amd.layer import QuantizedMoELayer
+
+    rng = np.random.default_rng(100 + B)
+    H, E, I, K = 2048, 32, 768, 8
+    banks, wr, sh, tq, tsh, wr_t = _build(dev, rng, H=H, E=E, I=I, K=K)
+    layer = QuantizedMoELayer.for_family("qwen3", wr_t, tq["gate"], tq["up"], tq["down"], top_k=K)
+    x = bf16_randn(rng, (B, H))
+    out, idx, w = layer(to_bf16(x, dev), return_routing=True)
+    torch.cuda.synchronize()
+    idx = from_dev(idx).astype(np.int64)
+    logits = O.dense_logits(x, wr)
+    p = O.softmax_precise_bf16(logits)
+    assert O.topk_is_valid(idx, p, K).all()
+    _, w_ref, _ = O.qwen_gating(logits, K, True, idx=idx)
+    assert O.bf16_ulp_diff(from_dev(w), w_ref).max() <= 1
+    ref = _oracle_out(x, idx, O.bf16_round(from_dev(w)), banks, None, "affine", 64, "native")
+    _cmp_out(from_dev(out), ref)
+
+
+def test_layer_lfm2_shape(dev):
+    """LFM2-8B-A1B shapes: H 2048, 32 experts, top-4, I 1792 (config 1)."""
+    import torch
+
+    from zmlx_amd.layer import QuantizedMoELayer
+
+    rng = np.random.default_rng(7)
+    H, E, I, K = 2048, 32, 1792, 4
+    banks, wr, sh, tq, tsh, wr_t = _build(dev, rng, H=H, E=E, I=I, K=K)
+    layer = QuantizedMoELayer.for_family("lfm2", wr_t, tq["gate"], tq["up"], tq["down"], top_k=K)
+    x = bf16_randn(rng, (1, H))
+    out, idx, w = layer(to_bf16(x, dev), return_routing=True)
+    torch.cuda.synchronize()
+    idx = from_dev(idx).astype(np.int64)
+    logits = O.dense_logits(x, wr)
+    assert O.topk_is_valid(idx, logits, K).all()
+    w_ref, _ = O.topk_gating_softmax(logits, K, None, True, idx=idx)
+    np.testing.assert_array_equal(from_dev(w), O.bf16_round(w_ref))
+    ref = _oracle_out(x, idx, O.bf16_round(w_ref), banks, None, "affine", 64, "native")
+    _cmp_out(from_dev(out), ref)
+
+
+@pytest.mark.parametrize("B", [1, 8])
+def test_layer_glm_mxfp4_shared(dev, B):
+    """GLM-4.7-Flash-like: 64 experts top-4 sigmoid + bias, shared expert,
+    I 1536, mxfp4, fp32 no-FMA combine (config 3)."""
+    import torch
+
+    from zmlx_amd.layer import QuantizedMoELayer
+
+    rng = np.random.default_rng(300 + B)
+    H, E, I, K = 2048, 64, 1536, 4
+    banks, wr, sh, tq, tsh, wr_t = _build(dev, rng, H=H, E=E, I=I, K=K, mode="mxfp4", gs=32, shared_I=1536)
+    bias = (rng.standard_normal(E) * 0.05).astype(np.float32)
+    layer = QuantizedMoELayer.for_family("glm", wr_t, tq["gate"], tq["up"], tq["down"], top_k=K,
+                                         router_bias=torch.from_numpy(bias).to(dev), group_size=32, mode="mxfp4",
+                                         routed_scaling_factor=1.8, shared=tsh)
+    x = bf16_randn(rng, (B, H))
+    out, idx, w = layer(to_bf16(x, dev), return_routing=True)
+    torch.cuda.synchronize()
+    logits = O.dense_logits(x, wr)
+    w_ref, i_ref = O.deepseek_router_topk_sigmoid(logits, bias, K, 1, 1, 1.8)
+    np.testing.assert_array_equal(from_dev(idx), i_ref)
+    np.testing.assert_allclose(from_dev(w), w_ref, rtol=1e-6, atol=1e-7)
+    ref = _oracle_out(x, i_ref, w_ref, banks, sh, "mxfp4", 32, "fp32_no_fma")
+    _cmp_out(from_dev(out), ref)
+
+
+def test_layer_deepseek_grouped(dev):
+    """DeepSeek-V3 routing (256 experts, 8 groups, top-4 groups, top-8,
+    scale 2.5) with reduced H/I for oracle speed; shared expert."""
+    import torch
+
+    from zmlx_amd.layer import QuantizedMoELayer
+
+    rng = np.random.default_rng(42)
+    H, E, I, K = 1024, 256, 256, 8
+    banks, wr, sh, tq, tsh, wr_t = _build(dev, rng, H=H, E=E, I=I, K=K, shared_I=512)
+    bias = (rng.standard_normal(E) * 0.05).astype(np.float32)
+    layer = QuantizedMoELayer.for_family("deepseek", wr_t, tq["gate"], tq["up"], tq["down"], top_k=K,
+                                         router_bias=torch.from_numpy(bias).to(dev), n_group=8, topk_group=4,
+                                         routed_scaling_factor=2.5, shared=tsh)
+    x = bf16_randn(rng, (3, H))
+    out, idx, w = layer(to_bf16(x, dev), return_routing=True)
+    torch.cuda.synchronize()
+    logits = O.dense_logits(x, wr)
+    w_ref, i_ref = O.deepseek_router_topk_sigmoid(logits, bias, K, 8, 4, 2.5)
+    np.testing.assert_array_equal(from_dev(idx), i_ref)
+    np.testing.assert_allclose(from_dev(w), w_ref, rtol=1e-6, atol=1e-6)
+    ref = _oracle_out(x, i_ref, w_ref, banks, sh, "affine", 64, "fp32_no_fma")
+    _cmp_out(from_dev(out), ref)
+
+
+def test_layer_zero_input_gives_zero(dev):
+    """x = 0 => logits 0 => every expert output is exactly 0 (g = u = 0)."""
+    import torch
+
+    from zmlx_amd.layer import QuantizedMoELayer
+
+    rng = np.random.default_rng(1)
+    H, E, I, K = 2048, 16, 768, 8
+    banks, wr, sh, tq, tsh, wr_t = _build(dev, rng, H=H, E=E, I=I, K=K)
+    layer = QuantizedMoELayer.for_family("qwen3", wr_t, tq["gate"], tq["up"], tq["down"], top_k=K)
+    out, idx, w = layer(torch.zeros((2, H), dtype=torch.bfloat16, device=dev), return_routing=True)
+    torch.cuda.synchronize()
+    assert (from_dev(out) == 0).all()
+    # uniform probabilities: lowest 8 indices, weights 1/8 each
+    assert (from_dev(idx) == np.arange(8)).all()
+    np.testing.assert_array_equal(from_dev(w), np.full((2, 8), 0.125, np.float32))
+
+
+def _layer_pair(dev, rng, family, *, H, E, I, K, mode="affine", gs=64, shared_I=0, **kw):
+    """The same layer built twice: single-launch kernel and kernel sequence."""
+    import torch
+
+    from zmlx_amd.layer import QuantizedMoELayer
+
+    banks, wr, sh, tq, tsh, wr_t = _build(dev, rng, H=H, E=E, I=I, K=K, mode=mode, gs=gs, shared_I=shared_I)
+    if "router_bias" in kw and kw["router_bias"] is not None:
+        kw["router_bias"] = torch.from_numpy(kw["router_bias"]).to(dev)
+    mk = lambda single: QuantizedMoELayer.for_family(  # noqa: E731
+        family, wr_t, tq["gate"], tq["up"], tq["down"], top_k=K, group_size=gs, mode=mode, shared=tsh,
+        single_launch=single, **kw)
+    return mk(True), mk(False)
+
+
+FUSED_CASES = [
+    ("qwen3", dict(H=2048, E=128, I=768, K=8), [1, 4, 8]),
+    ("lfm2", dict(H=2048, E=32, I=1792, K=4), [1, 3]),
+    ("glm", dict(H=2048, E=64, I=1536, K=4, mode="mxfp4", gs=32, shared_I=1536), [1, 8]),
+    ("deepseek", dict(H=1024, E=256, I=512, K=8, shared_I=512), [1, 2]),
+]
+
+
+@pytest.mark.parametrize("family,shape,batches", FUSED_CASES, ids=[c[0] for c in FUSED_CASES])
+def test_single_launch_matches_kernel_sequence(dev, family, shape, batches):
+    """The persistent single-launch layer kernel evaluates the same arithmetic
+    as the kernel sequence: outputs and routing bit-identical, for repeated
+    calls (barrier counters reset themselves) and ragged batch sizes."""
+    import torch
+
+    rng = np.random.default_rng(17)
+    kw = {}
+    if family in ("glm", "deepseek"):
+        kw["router_bias"] = (rng.standard_normal(shape["E"]) * 0.05).astype(np.float32)
+        kw["routed_scaling_factor"] = 2.5
+    if family == "deepseek":
+        kw.update(n_group=8, topk_group=4)
+    fused, multi = _layer_pair(dev, rng, family, **shape, **kw)
+    for B in batches:
+        x = to_bf16(bf16_randn(rng, (B, shape["H"])), dev)
+        for rep in range(3):
+            of, i_f, w_f = fused(x, return_routing=True)
+            om, i_m, w_m = multi(x, return_routing=True)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(from_dev(i_f), from_dev(i_m))
+            np.testing.assert_array_equal(from_dev(w_f), from_dev(w_m))
+            np.testing.assert_array_equal(from_dev(of), from_dev(om))
+    assert fused.sync_error() == 0

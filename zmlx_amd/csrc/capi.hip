@@ -1,0 +1,16 @@
+// Library-wide C entry points: version string and per-thread error message.
+#include <string>
+
+#include "zmoe_host.h"
+
+namespace zmoe {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+}  // namespace zmoe
+
+extern "C" const char* zmoe_version(void) { return "zmlx_amd 0.1.0 gfx950"; }
+
+extern "C" const char* zmoe_last_error(void) { return zmoe::g_last_error.c_str(); }

@@ -1,0 +1,184 @@
+// Whole MoE block forward (zmoe_moe_layer): router projection, gating,
+// gate/up + SwiGLU, down projection, combine and the optional shared expert,
+// enqueued back to back on one stream with all intermediates in the
+// caller's workspace.
+#include "zmoe_common.h"
+#include "zmoe_host.h"
+
+#include <cstdlib>
+#include <string>
+
+namespace zmoe {
+
+static size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+struct LayerWs {
+  void* logits;   // [B, E] bf16
+  uint32_t* idx;  // [B, K]
+  void* w;        // [B, K] bf16 or f32
+  void* act;      // [B*K, I] bf16
+  void* y;        // [B*K, H] bf16
+  void* sh_act;   // [B, I_s] bf16
+  void* sh_y;     // [B, H] bf16
+  size_t bytes;
+};
+
+static LayerWs layout_ws(const zmoe_layer_desc* d, int B, char* base) {
+  LayerWs ws{};
+  size_t off = 0;
+  auto take = [&](size_t n) {
+    void* p = base ? base + off : nullptr;
+    off += align_up(n);
+    return p;
+  };
+  const size_t BK = static_cast<size_t>(B) * d->top_k;
+  ws.logits = take(static_cast<size_t>(B) * d->n_experts * 2);
+  ws.idx = static_cast<uint32_t*>(take(BK * 4));
+  ws.w = take(BK * 4);
+  ws.act = take(BK * d->inter * 2);
+  ws.y = take(BK * d->hidden * 2);
+  ws.sh_act = take(static_cast<size_t>(B) * (d->shared_inter > 0 ? d->shared_inter : 0) * 2);
+  ws.sh_y = take(static_cast<size_t>(B) * (d->shared_inter > 0 ? d->hidden : 0) * 2);
+  ws.bytes = off;
+  return ws;
+}
+
+__global__ void k_weights_to_f32(const void* __restrict__ w, int is_f32, int n, float* __restrict__ out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n)
+    out[i] = is_f32 ? static_cast<const float*>(w)[i] : bf16_bits_to_f32(static_cast<const uint16_t*>(w)[i]);
+}
+
+static int validate_layer(const zmoe_layer_desc* d, int B) {
+  ZMOE_REQUIRE(d != nullptr, ZMOE_EINVAL_SHAPE, "[moe_layer] null descriptor.");
+  ZMOE_REQUIRE(B >= 0 && B <= 65535, ZMOE_EINVAL_SHAPE, "[moe_layer] B out of range.");
+  ZMOE_REQUIRE(d->hidden > 0 && d->n_experts > 0 && d->inter > 0, ZMOE_EINVAL_SHAPE, "[moe_layer] sizes must be positive.");
+  ZMOE_REQUIRE(d->top_k >= 1 && d->top_k <= 16 && d->top_k <= d->n_experts && d->n_experts <= 1024,
+               ZMOE_EINVAL_SHAPE, "[moe_layer] need 1 <= top_k <= min(16, E) and E <= 1024.");
+  ZMOE_REQUIRE(d->hidden % 256 == 0 && d->inter % 256 == 0, ZMOE_EINVAL_SHAPE,
+               "[moe_layer] hidden and inter must be multiples of 256.");
+  ZMOE_REQUIRE(d->shared_inter >= 0 && d->shared_inter % 256 == 0, ZMOE_EINVAL_SHAPE,
+               "[moe_layer] shared_inter must be a multiple of 256.");
+  ZMOE_REQUIRE(d->router_kind >= ZMOE_ROUTER_SOFTMAX_PROBS && d->router_kind <= ZMOE_ROUTER_SIGMOID_GROUPED,
+               ZMOE_EINVAL_SHAPE, "[moe_layer] unknown router kind.");
+  ZMOE_REQUIRE(d->combine_mode >= ZMOE_COMBINE_NATIVE && d->combine_mode <= ZMOE_COMBINE_NO_FMA, ZMOE_EINVAL_SHAPE,
+               "[moe_layer] unknown combine mode.");
+  ZMOE_REQUIRE(!(d->router_kind == ZMOE_ROUTER_SIGMOID_GROUPED && d->combine_mode == ZMOE_COMBINE_NATIVE),
+               ZMOE_EINVAL_DTYPE, "[moe_layer] the sigmoid router yields f32 weights: use an fp32 combine mode.");
+  if (d->router_kind == ZMOE_ROUTER_SIGMOID_GROUPED) {
+    ZMOE_REQUIRE(d->n_group >= 1 && d->n_group <= 64 && d->n_experts % d->n_group == 0 && d->topk_group >= 1 &&
+                     d->topk_group <= d->n_group,
+                 ZMOE_EINVAL_SHAPE, "[moe_layer] invalid n_group / topk_group.");
+    ZMOE_REQUIRE(d->router_bias != nullptr, ZMOE_EINVAL_SHAPE, "[moe_layer] sigmoid router needs a bias.");
+  }
+  ZMOE_REQUIRE(d->router_w && d->gate_w && d->up_w && d->down_w && d->gate_s && d->up_s && d->down_s,
+               ZMOE_EINVAL_SHAPE, "[moe_layer] null weight pointer.");
+  return ZMOE_OK;
+}
+
+}  // namespace zmoe
+
+using namespace zmoe;
+
+// Layer path selection: the fused single-launch kernel when it supports the
+// shape (decode batches), else the multi-kernel sequence.  ZMOE_LAYER_PATH=
+// "multi" forces the sequence (used by tests to compare the two paths).
+static bool use_fused(const zmoe_layer_desc* d, int B) {
+  static int forced = -1;
+  if (forced < 0) {
+    const char* e = getenv("ZMOE_LAYER_PATH");
+    forced = (e && std::string(e) == "multi") ? 0 : 1;
+  }
+  return forced == 1 && !(d->flags & ZMOE_LAYER_FORCE_MULTI) && fused_supported(d, B);
+}
+
+extern "C" size_t zmoe_moe_layer_workspace_size(const zmoe_layer_desc* desc, int B) {
+  if (!desc || B < 0) return 0;
+  const size_t multi = layout_ws(desc, B, nullptr).bytes;
+  const size_t fused = fused_supported(desc, B) ? fused_workspace_bytes(desc, B) : 0;
+  return 256 + (multi > fused ? multi : fused);
+}
+
+extern "C" size_t zmoe_moe_layer_trace_info(const zmoe_layer_desc* desc, int B, int* n_blocks, int* n_slots) {
+  if (!desc || !n_blocks || !n_slots || !fused_supported(desc, B)) return 0;
+  return fused_trace_info(desc, B, n_blocks, n_slots);
+}
+
+extern "C" int zmoe_moe_layer(void* stream, const zmoe_layer_desc* d, const void* x, int B, void* out,
+                              uint32_t* out_idx, float* out_w, void* workspace, size_t workspace_bytes) {
+  int rc = validate_layer(d, B);
+  if (rc) return rc;
+  if (B == 0) return ZMOE_OK;
+  const size_t need = zmoe_moe_layer_workspace_size(d, B);
+  ZMOE_REQUIRE(workspace != nullptr && workspace_bytes >= need, ZMOE_EINVAL_SHAPE,
+               "[moe_layer] workspace too small (need " + std::to_string(need) + " bytes).");
+  if (use_fused(d, B)) {
+    return launch_fused(as_stream(stream), d, x, B, out, out_idx, out_w, workspace);
+  }
+  // multi-kernel sequence: its buffers start after the 256-byte sync block
+  LayerWs ws = layout_ws(d, B, static_cast<char*>(workspace) + 256);
+  ZMOE_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(workspace) & 255) == 0,
+               ZMOE_EINVAL_SHAPE, "[moe_layer] x must be 16-byte and workspace 256-byte aligned.");
+  hipStream_t st = as_stream(stream);
+  const int H = d->hidden, E = d->n_experts, K = d->top_k, I = d->inter;
+  int gshift = 0;
+  if (d->quant_mode == ZMOE_Q_AFFINE) {
+    ZMOE_REQUIRE(d->group_size == 32 || d->group_size == 64 || d->group_size == 128, ZMOE_EUNSUPPORTED,
+                 "[moe_layer] group_size must be 32, 64 or 128.");
+    for (int v = d->group_size / 32; v > 1; v >>= 1) ++gshift;
+  } else {
+    ZMOE_REQUIRE(d->quant_mode == ZMOE_Q_MXFP4 && d->group_size == 32, ZMOE_EUNSUPPORTED,
+                 "[moe_layer] unsupported quantization.");
+  }
+  ZMOE_REQUIRE(d->bits == 4, ZMOE_EUNSUPPORTED, "[moe_layer] only 4-bit weights.");
+
+  // 1. router projection (bf16 logits, as the gate nn.Linear returns them)
+  rc = zmoe_dense_logits(stream, x, d->router_w, B, E, H, ZMOE_DT_BF16, ws.logits);
+  if (rc) return rc;
+  // 2. gating
+  int w_dtype = ZMOE_DT_BF16;
+  if (d->router_kind == ZMOE_ROUTER_SOFTMAX_PROBS) {
+    rc = zmoe_router_softmax_topk(stream, ws.logits, B, E, K, d->norm_topk_prob, ws.w, ws.idx);
+  } else if (d->router_kind == ZMOE_ROUTER_TOPK_LOGITS) {
+    rc = launch_topk_gating(st, ws.logits, ZMOE_DT_BF16, B, E, K, d->router_bias, d->norm_topk_prob, 1, ws.w, ws.idx);
+  } else {
+    w_dtype = ZMOE_DT_F32;
+    rc = launch_deepseek_router(st, ws.logits, ZMOE_DT_BF16, d->router_bias, B, E, K, d->n_group, d->topk_group,
+                                d->routed_scaling_factor, static_cast<float*>(ws.w), ws.idx);
+  }
+  if (rc) return rc;
+  // 3. routed experts: gate/up + SwiGLU, then down
+  rc = dispatch_qmv(true, stream, x, d->gate_w, d->gate_s, d->gate_b, d->up_w, d->up_s, d->up_b, nullptr, ws.idx, K,
+                    static_cast<int64_t>(B) * K, 1, I, H, d->quant_mode, gshift, ws.act);
+  if (rc) return rc;
+  rc = dispatch_qmv(false, stream, ws.act, d->down_w, d->down_s, d->down_b, nullptr, nullptr, nullptr, nullptr, ws.idx,
+                    1, static_cast<int64_t>(B) * K, 1, H, I, d->quant_mode, gshift, ws.y);
+  if (rc) return rc;
+  // 4. shared expert (dense SwiGLU MLP on every token)
+  const void* shared = nullptr;
+  if (d->shared_inter > 0) {
+    const int Is = d->shared_inter;
+    rc = dispatch_qmv(true, stream, x, d->sh_gate_w, d->sh_gate_s, d->sh_gate_b, d->sh_up_w, d->sh_up_s, d->sh_up_b,
+                      nullptr, nullptr, 1, B, 1, Is, H, d->quant_mode, gshift, ws.sh_act);
+    if (rc) return rc;
+    rc = dispatch_qmv(false, stream, ws.sh_act, d->sh_down_w, d->sh_down_s, d->sh_down_b, nullptr, nullptr, nullptr,
+                      nullptr, nullptr, 1, B, 1, H, Is, d->quant_mode, gshift, ws.sh_y);
+    if (rc) return rc;
+    shared = ws.sh_y;
+  }
+  // 5. combine (+ shared) -> bf16
+  rc = launch_combine(st, ws.y, ws.w, w_dtype, B, K, H, d->combine_mode, 1, shared, out);
+  if (rc) return rc;
+  if (out_idx) {
+    hipError_t e = hipMemcpyAsync(out_idx, ws.idx, static_cast<size_t>(B) * K * 4, hipMemcpyDeviceToDevice, st);
+    ZMOE_REQUIRE(e == hipSuccess, ZMOE_EHIP, std::string("[moe_layer] copy failed: ") + hipGetErrorString(e));
+  }
+  if (out_w) {
+    const int n = B * K;
+    hipLaunchKernelGGL(k_weights_to_f32, dim3((n + 255) / 256), dim3(256), 0, st, ws.w, w_dtype == ZMOE_DT_F32, n,
+                       out_w);
+    rc = check_launch("moe_layer");
+    if (rc) return rc;
+  }
+  return ZMOE_OK;
+}

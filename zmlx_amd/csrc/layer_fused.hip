@@ -1,0 +1,674 @@
+// Single-launch MoE decode layer (the fused path of zmoe_moe_layer).
+//
+// One persistent grid of G = (#CUs) workgroups x 8 waves, every workgroup
+// resident at once, runs the whole block in four phases separated by two
+// grid barriers:
+//
+//   R  router projection: the E x (H/512) (row, 1 KiB chunk) units are
+//      spread over all waves; partial dots go to the workspace; meanwhile
+//      x is staged in LDS.
+//      -- barrier 1 --
+//   T  routing: every workgroup reduces the partials in a fixed order and
+//      routes each token (wave b <-> token b) -- redundantly, which is
+//      cheaper than a third barrier -- then gives the selected experts
+//      (plus the shared expert) unit slots.
+//   A  gate/up + SwiGLU: rows of the units are spread over all waves; act
+//      rows go to the workspace.  Each wave then issues its first batch of
+//      down-projection weight loads *before* waiting, so that stream
+//      overlaps the barrier.
+//      -- barrier 2 --
+//   D  down projection: each wave owns output rows h for all units, so the
+//      k-ordered combine and the shared-expert add happen in-workgroup and
+//      each output element is written once.
+//
+// Code size matters here: the kernel runs each phase once per wave, so it is
+// written with rolled loops (per-token accumulators live in LDS) to stay
+// within the instruction cache.  Cross-workgroup data (router partials,
+// act rows, barrier words) use device-scope atomic accesses, which are
+// coherent across the XCDs without cache-wide writeback/invalidate.  A
+// barrier: every workgroup bumps one counter; the last arrival resets it and
+// raises one flag per workgroup (own 128-byte line, so no polling hot spot).
+// Every wait is bounded (on timeout: sticky error word, continue), so the
+// grid always drains.  The arithmetic is the multi-kernel path's (same dot
+// products, reduction trees, routing code and combine): results are
+// bit-identical to it.
+#include "zmoe_common.h"
+#include "zmoe_combine.h"
+#include "zmoe_host.h"
+#include "zmoe_route.h"
+
+namespace zmoe {
+
+constexpr int kFThreads = 512;
+constexpr int kFWaves = kFThreads / kWave;
+constexpr int kFMaxB = 8;                 // tokens per call on the fused path
+constexpr int kFMaxUnits = kFMaxB * kMaxTopK + 1;
+constexpr int kChunkA = 4;                // (row-group, segment) items per batch, phase A
+constexpr int kChunkD = 8;                // (slot-group, segment) items per batch, phase D
+constexpr unsigned kSpinLimit = 1u << 21;
+constexpr int kTraceSlots = 16;
+constexpr int kFlagStride = 32;           // uint32 words between barrier flags (128 B)
+
+struct FusedParams {
+  int H, E, K, I, Is, B;
+  int gshift, combine_mode;
+  RouteArgs route;
+  int LH, LI;            // lanes per row for K_in = H / K_in = I (= Is)
+  const uint16_t* x;
+  uint16_t* out;
+  const uint16_t* wr;
+  const uint32_t* w[6];  // gate, up, down, sh_gate, sh_up, sh_down
+  const void* s[6];
+  const void* b[6];
+  unsigned* bar;         // [0] counter 1, [16] counter 2, [32] error word
+  unsigned* flags;       // [2][G][kFlagStride]
+  float* rpart;          // [B][E][NC]
+  float* act;            // [B*K + B][act_stride] (bf16 values held in f32)
+  int act_stride;
+  uint32_t* out_idx;
+  float* out_w;
+  unsigned long long* trace;  // nullable: [G][kTraceSlots] realtime stamps
+};
+
+struct FusedLds {
+  int ulist[kFMaxUnits];   // expert of each unit (slot order = expert order)
+  int ucount[kFMaxUnits];
+  int upairs[kFMaxUnits][kFMaxB];
+  int nunits;              // routed units; the shared unit (if any) is index nunits
+  int slot_of[1024];
+  RouteLds route[kFMaxB];
+};
+
+__device__ __forceinline__ void trace_mark(const FusedParams& p, int slot) {
+  if (p.trace && threadIdx.x == 0) p.trace[blockIdx.x * kTraceSlots + slot] = wall_clock64();
+}
+
+__device__ __forceinline__ void dev_store(float* a, float v) {
+  __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float dev_load(const float* a) {
+  return __hip_atomic_load(const_cast<float*>(a), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ void grid_sync(const FusedParams& p, int which) {
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's device-scope stores are performed
+  __syncthreads();
+  if (threadIdx.x < kWave) {
+    const unsigned G = gridDim.x;
+    unsigned* cnt = p.bar + 16 * which;
+    unsigned* fl = p.flags + static_cast<size_t>(which) * G * kFlagStride;
+    int last = 0;
+    if (threadIdx.x == 0) last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1;
+    last = __shfl(last, 0);
+    if (last) {
+      if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (unsigned i = threadIdx.x; i < G; i += kWave)
+        __hip_atomic_store(fl + static_cast<size_t>(i) * kFlagStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (threadIdx.x == 0) {
+      unsigned* mine = fl + static_cast<size_t>(blockIdx.x) * kFlagStride;
+      unsigned n = 0;
+      while (__hip_atomic_load(mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
+        if (++n > kSpinLimit) {
+          __hip_atomic_fetch_or(p.bar + 32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      __hip_atomic_store(mine, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __syncthreads();
+}
+
+// Cross-lane sum over aligned groups of L lanes (L a power of two <= 64);
+// same butterfly order as wave_sum_width<L>.
+__device__ __forceinline__ float lanes_sum(float v, int L) {
+  for (int o = L >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// x rows (bf16) -> LDS tile in the layout of qmv.hip (stage_x_row).
+template <int QMODE>
+__device__ void stage_rows_lds(const uint16_t* __restrict__ src, int64_t src_stride, int nrows, int S, uint32_t* xs,
+                               float* sx) {
+  for (int i = threadIdx.x; i < nrows * S * 4; i += blockDim.x) {
+    const int r = i / (S * 4);
+    const int rem = i - r * S * 4;
+    const int s = rem >> 2, j = rem & 3;
+    const uint4 v = *reinterpret_cast<const uint4*>(src + r * src_stride + s * 32 + j * 8);
+    uint4 o;
+    if (QMODE == ZMOE_Q_AFFINE) {
+      o.x = (v.x & 0xFFFFu) | (v.z << 16);
+      o.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
+      o.z = (v.y & 0xFFFFu) | (v.w << 16);
+      o.w = (v.y >> 16) | (v.w & 0xFFFF0000u);
+    } else {
+      o = v;
+    }
+    *reinterpret_cast<uint4*>(xs + ((r * 4 + j) * S + s) * 4) = o;
+  }
+  if (QMODE == ZMOE_Q_AFFINE) {
+    for (int i = threadIdx.x; i < nrows * S; i += blockDim.x) {
+      const int r = i / S, s = i - r * S;
+      const uint4* q = reinterpret_cast<const uint4*>(src + r * src_stride + s * 32);
+      float acc = 0.0f;
+      for (int w = 0; w < 4; ++w) {
+        const uint4 v = q[w];
+        acc += bf16_bits_to_f32(v.x & 0xFFFFu) + bf16_bits_to_f32(v.x >> 16);
+        acc += bf16_bits_to_f32(v.y & 0xFFFFu) + bf16_bits_to_f32(v.y >> 16);
+        acc += bf16_bits_to_f32(v.z & 0xFFFFu) + bf16_bits_to_f32(v.z >> 16);
+        acc += bf16_bits_to_f32(v.w & 0xFFFFu) + bf16_bits_to_f32(v.w >> 16);
+      }
+      sx[r * S + s] = acc;
+    }
+  }
+}
+
+// act rows (f32 holding bf16 values, device-coherent loads) -> same layout.
+template <int QMODE>
+__device__ void stage_act_lds(const float* __restrict__ src, int64_t src_stride, int nrows, int S, uint32_t* xs,
+                              float* sx) {
+  for (int i = threadIdx.x; i < nrows * S * 4; i += blockDim.x) {
+    const int r = i / (S * 4);
+    const int rem = i - r * S * 4;
+    const int s = rem >> 2, j = rem & 3;
+    const float* q = src + r * src_stride + s * 32 + j * 8;
+    uint32_t e[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) e[t] = __float_as_uint(dev_load(q + t)) >> 16;
+    uint4 o;
+    if (QMODE == ZMOE_Q_AFFINE) {
+      o.x = e[0] | (e[4] << 16);
+      o.y = e[1] | (e[5] << 16);
+      o.z = e[2] | (e[6] << 16);
+      o.w = e[3] | (e[7] << 16);
+    } else {
+      o.x = e[0] | (e[1] << 16);
+      o.y = e[2] | (e[3] << 16);
+      o.z = e[4] | (e[5] << 16);
+      o.w = e[6] | (e[7] << 16);
+    }
+    *reinterpret_cast<uint4*>(xs + ((r * 4 + j) * S + s) * 4) = o;
+  }
+  if (QMODE == ZMOE_Q_AFFINE) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < nrows * S; i += blockDim.x) {
+      const int r = i / S, s = i - r * S;
+      float acc = 0.0f;
+      for (int w = 0; w < 4; ++w) {
+        // pairs (e0,e4) (e1,e5) (e2,e6) (e3,e7); summed as in stage_x_row:
+        // (e0+e1) (e2+e3) (e4+e5) (e6+e7)
+        const uint4 o = *reinterpret_cast<const uint4*>(xs + ((r * 4 + w) * S + s) * 4);
+        acc += bf16_bits_to_f32(o.x & 0xFFFFu) + bf16_bits_to_f32(o.y & 0xFFFFu);
+        acc += bf16_bits_to_f32(o.z & 0xFFFFu) + bf16_bits_to_f32(o.w & 0xFFFFu);
+        acc += bf16_bits_to_f32(o.x >> 16) + bf16_bits_to_f32(o.y >> 16);
+        acc += bf16_bits_to_f32(o.z >> 16) + bf16_bits_to_f32(o.w >> 16);
+      }
+      sx[r * S + s] = acc;
+    }
+  }
+}
+
+template <int QMODE>
+__device__ __forceinline__ float seg_dot_lds(const uint4 w, const uint32_t* xs, int S, int r, int s) {
+  const uint4 x0 = *reinterpret_cast<const uint4*>(xs + ((r * 4 + 0) * S + s) * 4);
+  const uint4 x1 = *reinterpret_cast<const uint4*>(xs + ((r * 4 + 1) * S + s) * 4);
+  const uint4 x2 = *reinterpret_cast<const uint4*>(xs + ((r * 4 + 2) * S + s) * 4);
+  const uint4 x3 = *reinterpret_cast<const uint4*>(xs + ((r * 4 + 3) * S + s) * 4);
+  const uint32_t a0[4] = {x0.x, x0.y, x0.z, x0.w};
+  const uint32_t a1[4] = {x1.x, x1.y, x1.z, x1.w};
+  const uint32_t a2[4] = {x2.x, x2.y, x2.z, x2.w};
+  const uint32_t a3[4] = {x3.x, x3.y, x3.z, x3.w};
+  float v = 0.0f;
+  if (QMODE == ZMOE_Q_AFFINE) {
+    v = dot_affine4_word(w.x, a0, v);
+    v = dot_affine4_word(w.y, a1, v);
+    v = dot_affine4_word(w.z, a2, v);
+    v = dot_affine4_word(w.w, a3, v);
+  } else {
+    v = dot_mxfp4_word(w.x, a0, v);
+    v = dot_mxfp4_word(w.y, a1, v);
+    v = dot_mxfp4_word(w.z, a2, v);
+    v = dot_mxfp4_word(w.w, a3, v);
+  }
+  return v;
+}
+
+template <int QMODE>
+__device__ __forceinline__ void seg_param(const void* __restrict__ scales, const void* __restrict__ biases, int64_t idx,
+                                          float& s, float& c) {
+  if (QMODE == ZMOE_Q_AFFINE) {
+    s = bf16_bits_to_f32(static_cast<const uint16_t*>(scales)[idx]);
+    c = bf16_bits_to_f32(static_cast<const uint16_t*>(biases)[idx]) - 128.0f * s;
+  } else {
+    s = e8m0_to_f32(static_cast<const uint8_t*>(scales)[idx]);
+    c = 0.0f;
+  }
+}
+
+struct UnitPtr {
+  const uint32_t* w;
+  const void* s;
+  const void* b;
+};
+
+// Weights of unit u for matrix m (0 gate, 1 up, 2 down): routed expert
+// ulist[u] or, for u == nunits, the shared expert.
+template <int QMODE>
+__device__ __forceinline__ UnitPtr unit_ptr(const FusedParams& p, const FusedLds& L, int u, int m) {
+  UnitPtr r;
+  if (u < L.nunits) {
+    const int64_t e = L.ulist[u];
+    const int64_t N = (m == 2) ? p.H : p.I;
+    const int64_t Kin = (m == 2) ? p.I : p.H;
+    const int64_t ppr = (QMODE == ZMOE_Q_AFFINE) ? ((Kin >> 5) >> p.gshift) : (Kin >> 5);
+    r.w = p.w[m] + e * N * (Kin >> 3);
+    r.s = static_cast<const char*>(p.s[m]) + e * N * ppr * ((QMODE == ZMOE_Q_AFFINE) ? 2 : 1);
+    r.b = (QMODE == ZMOE_Q_AFFINE) ? static_cast<const void*>(static_cast<const char*>(p.b[m]) + e * N * ppr * 2)
+                                   : nullptr;
+  } else {
+    r.w = p.w[3 + m];
+    r.s = p.s[3 + m];
+    r.b = p.b[3 + m];
+  }
+  return r;
+}
+
+template <int QMODE>
+__global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  FusedLds& L = *reinterpret_cast<FusedLds*>(smem);
+  unsigned char* big = smem + ((sizeof(FusedLds) + 15) & ~static_cast<size_t>(15));
+
+  const int wave = threadIdx.x / kWave;
+  const int lane = __lane_id();
+  const int G = gridDim.x;
+  const int W = G * kFWaves;
+  const int gw = blockIdx.x * kFWaves + wave;
+  const int B = p.B;
+  const int E = p.E;
+  const int NC = p.H >> 9;
+  const int S_H = p.H >> 5, S_I = p.I >> 5;
+  const bool has_shared = p.Is > 0;
+  trace_mark(p, 0);
+  if (p.trace && threadIdx.x == 0) p.trace[blockIdx.x * kTraceSlots + 13] = clock64();
+
+  // phase R..A LDS: x tile, x sums, router rows, phase-A accumulators
+  uint32_t* xs = reinterpret_cast<uint32_t*>(big);
+  float* sx = reinterpret_cast<float*>(xs + static_cast<size_t>(B) * S_H * 16);
+  float* rv = sx + static_cast<size_t>(B) * S_H;          // [B][E]
+  float* raff = rv + static_cast<size_t>(B) * E;          // [B][E]
+  float* accA = raff + static_cast<size_t>(B) * E;        // [waves][2][B][64]
+
+  // ---------------- phase R: router partials ----------------
+  for (int u = gw; u < E * NC; u += W) {
+    const int e = u / NC, c = u - e * NC;
+    const uint4 wv = *reinterpret_cast<const uint4*>(p.wr + static_cast<int64_t>(e) * p.H + c * 512 + lane * 8);
+    for (int b = 0; b < B; ++b) {
+      const uint4 xv = *reinterpret_cast<const uint4*>(p.x + static_cast<int64_t>(b) * p.H + c * 512 + lane * 8);
+      float a = 0.0f;
+      a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv.x), __builtin_bit_cast(bf16x2_t, xv.x), a, false);
+      a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv.y), __builtin_bit_cast(bf16x2_t, xv.y), a, false);
+      a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv.z), __builtin_bit_cast(bf16x2_t, xv.z), a, false);
+      a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv.w), __builtin_bit_cast(bf16x2_t, xv.w), a, false);
+      a = wave_sum(a);
+      if (lane == 0) dev_store(p.rpart + (static_cast<int64_t>(b) * E + e) * NC + c, a);
+    }
+  }
+  stage_rows_lds<QMODE>(p.x, p.H, B, S_H, xs, sx);
+  trace_mark(p, 1);
+  grid_sync(p, 0);
+  trace_mark(p, 2);
+
+  // ---------------- phase T: routing (wave b <-> token b) ----------------
+  if (wave < B) {
+    const int b = wave;
+    float* v = rv + static_cast<size_t>(b) * E;
+    const float* rp = p.rpart + static_cast<int64_t>(b) * E * NC;
+    for (int e = lane; e < E; e += kWave) {
+      float a = 0.0f;
+      for (int c = 0; c < NC; ++c) a += dev_load(rp + e * NC + c);  // chunks in order
+      v[e] = round_bf16(a);  // the gate Linear returns bf16 logits
+    }
+    wave_lds_sync();
+    trace_mark(p, 3);
+    route_row(p.route, v, raff + static_cast<size_t>(b) * E, L.route[b]);
+    trace_mark(p, 4);
+    if (blockIdx.x == 0 && lane < p.K) {
+      if (p.out_idx) p.out_idx[b * p.K + lane] = static_cast<uint32_t>(L.route[b].sel[lane]);
+      if (p.out_w) p.out_w[b * p.K + lane] = L.route[b].w[lane];
+    }
+  }
+  for (int e = threadIdx.x; e < E; e += blockDim.x) L.slot_of[e] = -1;
+  __syncthreads();
+  const int npairs = B * p.K;
+  for (int q = threadIdx.x; q < npairs; q += blockDim.x) L.slot_of[L.route[q / p.K].sel[q % p.K]] = 0;
+  __syncthreads();
+  if (wave == 0) {  // unit slots in expert order
+    int base = 0;
+    for (int e0 = 0; e0 < E; e0 += kWave) {
+      const int e = e0 + lane;
+      const bool f = e < E && L.slot_of[e] == 0;
+      const uint64_t m = __ballot(f);
+      if (f) {
+        const int pos = base + __popcll(m & lanes_below_mask(lane));
+        L.slot_of[e] = pos;
+        L.ulist[pos] = e;
+        L.ucount[pos] = 0;
+      }
+      base += __popcll(m);
+    }
+    if (lane == 0) {
+      L.nunits = base;
+      if (has_shared) L.ucount[base] = B;
+    }
+  }
+  __syncthreads();
+  for (int q = threadIdx.x; q < npairs; q += blockDim.x) {
+    const int u = L.slot_of[L.route[q / p.K].sel[q % p.K]];
+    L.upairs[u][atomicAdd(&L.ucount[u], 1)] = q;
+  }
+  if (has_shared && threadIdx.x < B) L.upairs[L.nunits][threadIdx.x] = npairs + threadIdx.x;
+  __syncthreads();
+  const int U = L.nunits;
+  const int Uall = U + (has_shared ? 1 : 0);
+  trace_mark(p, 5);
+
+  // ---------------- phase A: gate/up + SwiGLU ----------------
+  {
+    const int LH = p.LH, RPI = kWave / LH;
+    const int rs = lane / LH, li = lane % LH;
+    const int T = S_H / LH;
+    const int rg_routed = p.I / RPI;
+    const int rg_total = U * rg_routed + (has_shared ? p.Is / RPI : 0);
+    const int per = (rg_total + W - 1) / W;
+    const int g0 = gw * per, g1 = min(rg_total, g0 + per);
+    const int n_items = max(0, g1 - g0) * T;
+    const int64_t wpr = p.H >> 3;
+    const int64_t ppr = (QMODE == ZMOE_Q_AFFINE) ? (S_H >> p.gshift) : S_H;
+    float* ag = accA + (static_cast<size_t>(wave) * 2 * B) * kWave + lane;  // [tk] stride 64
+    float* au = ag + static_cast<size_t>(B) * kWave;
+    for (int base = 0; base < n_items; base += kChunkA) {
+      uint4 wg[kChunkA], wu[kChunkA];
+      float sg[kChunkA], cg[kChunkA], su[kChunkA], cu[kChunkA];
+#pragma unroll
+      for (int j = 0; j < kChunkA; ++j) {
+        const int it = base + j;
+        if (it < n_items) {
+          const int gi = it / T, t = it - gi * T;
+          const int g = g0 + gi;
+          const int u = g < U * rg_routed ? g / rg_routed : U;
+          const int row = (g - (u < U ? u * rg_routed : U * rg_routed)) * RPI + rs;
+          const int s = t * LH + li;
+          const UnitPtr pg = unit_ptr<QMODE>(p, L, u, 0);
+          const UnitPtr pu = unit_ptr<QMODE>(p, L, u, 1);
+          wg[j] = *reinterpret_cast<const uint4*>(pg.w + row * wpr + s * 4);
+          wu[j] = *reinterpret_cast<const uint4*>(pu.w + row * wpr + s * 4);
+          const int pi = (QMODE == ZMOE_Q_AFFINE) ? (s >> p.gshift) : s;
+          seg_param<QMODE>(pg.s, pg.b, row * ppr + pi, sg[j], cg[j]);
+          seg_param<QMODE>(pu.s, pu.b, row * ppr + pi, su[j], cu[j]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kChunkA; ++j) {
+        const int it = base + j;
+        if (it < n_items) {
+          const int gi = it / T, t = it - gi * T;
+          const int g = g0 + gi;
+          const int u = g < U * rg_routed ? g / rg_routed : U;
+          const int s = t * LH + li;
+          const int nt = L.ucount[u];
+          for (int tk = 0; tk < nt; ++tk) {
+            const int q = L.upairs[u][tk];
+            const int b = (u < U) ? q / p.K : q - npairs;
+            const float xsum = (QMODE == ZMOE_Q_AFFINE) ? sx[b * S_H + s] : 0.0f;
+            const float g_prev = t == 0 ? 0.0f : ag[tk * kWave];
+            const float u_prev = t == 0 ? 0.0f : au[tk * kWave];
+            ag[tk * kWave] = seg_accum<QMODE>(g_prev, sg[j], cg[j], seg_dot_lds<QMODE>(wg[j], xs, S_H, b, s), xsum);
+            au[tk * kWave] = seg_accum<QMODE>(u_prev, su[j], cu[j], seg_dot_lds<QMODE>(wu[j], xs, S_H, b, s), xsum);
+          }
+          if (base == 0 && j == 0) trace_mark(p, 6);
+          if (t == T - 1) {  // row-group complete: reduce, SwiGLU, store act
+            const int row = (g - (u < U ? u * rg_routed : U * rg_routed)) * RPI + rs;
+            for (int tk = 0; tk < nt; ++tk) {
+              const float gv = lanes_sum(ag[tk * kWave], LH);
+              const float uv = lanes_sum(au[tk * kWave], LH);
+              if (li == 0) {
+                const int q = L.upairs[u][tk];
+                dev_store(p.act + static_cast<int64_t>(q) * p.act_stride + row,
+                          bf16_bits_to_f32(swiglu_bf16(round_bf16(gv), round_bf16(uv))));
+              }
+            }
+          }
+        }
+      }
+    }
+  }
+  trace_mark(p, 7);
+
+  // ---------------- phase D setup: first down batch before the barrier ----------------
+  const int LI = p.LI, RPID = kWave / LI;
+  const int rsD = lane / LI, liD = lane % LI;
+  const int TD = S_I / LI;
+  const int rows_per_wave = (p.H + W - 1) / W;
+  const int h0 = gw * rows_per_wave;
+  const int nrows = max(0, min(p.H, h0 + rows_per_wave) - h0);
+  const int slots = nrows * Uall;  // (h_local, unit), unit fastest
+  const int n_itemsD = ((slots + RPID - 1) / RPID) * TD;
+  const int64_t wprD = p.I >> 3;
+  const int64_t pprD = (QMODE == ZMOE_Q_AFFINE) ? (S_I >> p.gshift) : S_I;
+  uint4 wd[kChunkD];
+  float sd[kChunkD], cd[kChunkD];
+#define ZMOE_LOAD_DOWN(BASE)                                                              \
+  _Pragma("unroll") for (int j = 0; j < kChunkD; ++j) {                                  \
+    const int it = (BASE) + j;                                                            \
+    if (it < n_itemsD) {                                                                  \
+      const int gi = it / TD, t = it - gi * TD;                                           \
+      const int slot = min(gi * RPID + rsD, slots - 1);                                   \
+      const int hl = slot / Uall, u = slot - hl * Uall;                                   \
+      const UnitPtr pd = unit_ptr<QMODE>(p, L, u, 2);                                     \
+      const int s = t * LI + liD;                                                         \
+      const int64_t row = h0 + hl;                                                        \
+      wd[j] = *reinterpret_cast<const uint4*>(pd.w + row * wprD + s * 4);                 \
+      const int pi = (QMODE == ZMOE_Q_AFFINE) ? (s >> p.gshift) : s;                      \
+      seg_param<QMODE>(pd.s, pd.b, row * pprD + pi, sd[j], cd[j]);                        \
+    }                                                                                     \
+  }
+  ZMOE_LOAD_DOWN(0)
+  trace_mark(p, 8);
+
+  grid_sync(p, 1);
+  trace_mark(p, 9);
+
+  // ---------------- phase D: down projection ----------------
+  const int P0 = npairs;
+  const int Ptot = npairs + (has_shared ? B : 0);
+  uint32_t* as = reinterpret_cast<uint32_t*>(big);
+  float* asx = reinterpret_cast<float*>(as + static_cast<size_t>(Ptot) * S_I * 16);
+  float* ybuf = asx + static_cast<size_t>(Ptot) * S_I;                         // [wg rows][Ptot]
+  float* accD = ybuf + static_cast<size_t>(kFWaves) * rows_per_wave * Ptot;   // [waves][B][64]
+  stage_act_lds<QMODE>(p.act, p.act_stride, Ptot, S_I, as, asx);
+  __syncthreads();
+  trace_mark(p, 10);
+  float* ad = accD + static_cast<size_t>(wave) * B * kWave + lane;
+  for (int base = 0; base < n_itemsD; base += kChunkD) {
+    if (base > 0) {
+      ZMOE_LOAD_DOWN(base)
+    }
+#pragma unroll
+    for (int j = 0; j < kChunkD; ++j) {
+      const int it = base + j;
+      if (it < n_itemsD) {
+        const int gi = it / TD, t = it - gi * TD;
+        const int slot_raw = gi * RPID + rsD;
+        const int slot = min(slot_raw, slots - 1);
+        const int hl = slot / Uall, u = slot - hl * Uall;
+        const int s = t * LI + liD;
+        const int nt = L.ucount[u];
+        for (int tk = 0; tk < nt; ++tk) {
+          const int q = L.upairs[u][tk];
+          const float xsum = (QMODE == ZMOE_Q_AFFINE) ? asx[q * S_I + s] : 0.0f;
+          const float prev = t == 0 ? 0.0f : ad[tk * kWave];
+          ad[tk * kWave] = seg_accum<QMODE>(prev, sd[j], cd[j], seg_dot_lds<QMODE>(wd[j], as, S_I, q, s), xsum);
+        }
+        if (t == TD - 1) {
+          for (int tk = 0; tk < nt; ++tk) {
+            const float y = lanes_sum(ad[tk * kWave], LI);
+            if (liD == 0 && slot_raw < slots) ybuf[(wave * rows_per_wave + hl) * Ptot + L.upairs[u][tk]] = round_bf16(y);
+          }
+        }
+      }
+    }
+  }
+#undef ZMOE_LOAD_DOWN
+  __syncthreads();
+  trace_mark(p, 11);
+
+  // ---------------- combine (+ shared expert) ----------------
+  const int wg_row0 = blockIdx.x * kFWaves * rows_per_wave;
+  for (int i = threadIdx.x; i < kFWaves * rows_per_wave * B; i += blockDim.x) {
+    const int r = i / B, b = i - r * B;
+    const int h = wg_row0 + r;
+    if (h >= p.H) continue;
+    const float* yr = ybuf + r * Ptot + b * p.K;
+    const float* wk = L.route[b].w;
+    float o = round_bf16(combine_one(p.combine_mode, p.K, [&](int k) { return yr[k]; }, [&](int k) { return wk[k]; }));
+    if (has_shared) o = add_nofma(o, ybuf[r * Ptot + P0 + b]);
+    p.out[static_cast<int64_t>(b) * p.H + h] = static_cast<uint16_t>(f32_to_bf16_bits(o));
+  }
+  trace_mark(p, 12);
+  if (p.trace && threadIdx.x == 0) p.trace[blockIdx.x * kTraceSlots + 14] = clock64();
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+static int g_num_cu = 0;
+
+static int num_cus() {
+  if (g_num_cu == 0) {
+    int dev = 0;
+    hipDeviceProp_t prop;
+    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
+      g_num_cu = prop.multiProcessorCount;
+    if (g_num_cu <= 0) g_num_cu = 1;
+  }
+  return g_num_cu;
+}
+
+static size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+size_t fused_lds_bytes(const zmoe_layer_desc* d, int B) {
+  const int S_H = d->hidden / 32, S_I = d->inter / 32;
+  const int Ptot = B * d->top_k + (d->shared_inter > 0 ? B : 0);
+  const int G = num_cus();
+  const int rows_per_wave = (d->hidden + G * kFWaves - 1) / (G * kFWaves);
+  const size_t front = static_cast<size_t>(B) * S_H * 68 + static_cast<size_t>(B) * d->n_experts * 8 +
+                       static_cast<size_t>(kFWaves) * 2 * B * kWave * 4;
+  const size_t back = static_cast<size_t>(Ptot) * S_I * 68 + static_cast<size_t>(kFWaves) * rows_per_wave * Ptot * 4 +
+                      static_cast<size_t>(kFWaves) * B * kWave * 4;
+  return ((sizeof(FusedLds) + 15) & ~static_cast<size_t>(15)) + (front > back ? front : back);
+}
+
+bool fused_supported(const zmoe_layer_desc* d, int B) {
+  if (B < 1 || B > kFMaxB) return false;
+  if (d->hidden % 512 != 0) return false;
+  if (d->shared_inter > 0 && d->shared_inter != d->inter) return false;
+  if (d->n_experts > 1024 || d->top_k > kMaxTopK) return false;
+  if (fused_lds_bytes(d, B) > 160 * 1024) return false;
+  return true;
+}
+
+// workspace: [0,256) barrier words | flags 2 x G x 128 B | rpart | act | trace
+static size_t off_flags() { return 256; }
+static size_t off_rpart() { return align256(off_flags() + 2ull * num_cus() * kFlagStride * 4); }
+static size_t off_act(const zmoe_layer_desc* d, int B) {
+  return align256(off_rpart() + static_cast<size_t>(B) * d->n_experts * (d->hidden / 512) * 4);
+}
+static size_t off_trace(const zmoe_layer_desc* d, int B) {
+  const int stride = d->inter > d->shared_inter ? d->inter : d->shared_inter;
+  const size_t Ptot = static_cast<size_t>(B) * d->top_k + (d->shared_inter > 0 ? B : 0);
+  return align256(off_act(d, B) + Ptot * stride * 4);
+}
+
+size_t fused_workspace_bytes(const zmoe_layer_desc* d, int B) {
+  return off_trace(d, B) + static_cast<size_t>(num_cus()) * kTraceSlots * 8;
+}
+
+size_t fused_trace_info(const zmoe_layer_desc* d, int B, int* n_blocks, int* n_slots) {
+  *n_blocks = num_cus();
+  *n_slots = kTraceSlots;
+  return off_trace(d, B);
+}
+
+template <int QMODE>
+static int launch_fused_t(hipStream_t st, const FusedParams& fp, size_t lds) {
+  static bool prepared = false;
+  int occ = 0;
+  if (!prepared) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_moe_decode<QMODE>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    prepared = true;
+  }
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(&k_moe_decode<QMODE>),
+                                                   kFThreads, lds) != hipSuccess ||
+      occ < 1) {
+    return fail(ZMOE_EUNSUPPORTED, "[moe_layer] single-launch kernel cannot be resident on every CU");
+  }
+  hipLaunchKernelGGL((k_moe_decode<QMODE>), dim3(num_cus()), dim3(kFThreads), lds, st, fp);
+  return check_launch("moe_layer(single launch)");
+}
+
+int launch_fused(hipStream_t st, const zmoe_layer_desc* d, const void* x, int B, void* out, uint32_t* out_idx,
+                 float* out_w, void* workspace) {
+  FusedParams fp{};
+  fp.H = d->hidden;
+  fp.E = d->n_experts;
+  fp.K = d->top_k;
+  fp.I = d->inter;
+  fp.Is = d->shared_inter;
+  fp.B = B;
+  int gs = 0;
+  for (int v = d->group_size / 32; v > 1; v >>= 1) ++gs;
+  fp.gshift = d->quant_mode == ZMOE_Q_AFFINE ? gs : 0;
+  fp.combine_mode = d->combine_mode;
+  const bool grouped = d->router_kind == ZMOE_ROUTER_SIGMOID_GROUPED;
+  fp.route.kind = d->router_kind;
+  fp.route.E = d->n_experts;
+  fp.route.k = d->top_k;
+  fp.route.norm = d->norm_topk_prob;
+  fp.route.n_group = grouped ? d->n_group : 1;
+  fp.route.topk_group = grouped ? d->topk_group : 1;
+  fp.route.scale = grouped ? d->routed_scaling_factor : 1.0f;
+  fp.route.bias = d->router_bias;
+  fp.route.w_bf16 = 1;
+  fp.LH = gcd_int(d->hidden / 32, kWave);
+  fp.LI = gcd_int(d->inter / 32, kWave);
+  fp.x = static_cast<const uint16_t*>(x);
+  fp.out = static_cast<uint16_t*>(out);
+  fp.wr = static_cast<const uint16_t*>(d->router_w);
+  const uint32_t* ws[6] = {d->gate_w, d->up_w, d->down_w, d->sh_gate_w, d->sh_up_w, d->sh_down_w};
+  const void* ss[6] = {d->gate_s, d->up_s, d->down_s, d->sh_gate_s, d->sh_up_s, d->sh_down_s};
+  const void* bs[6] = {d->gate_b, d->up_b, d->down_b, d->sh_gate_b, d->sh_up_b, d->sh_down_b};
+  for (int i = 0; i < 6; ++i) {
+    fp.w[i] = ws[i];
+    fp.s[i] = ss[i];
+    fp.b[i] = bs[i];
+  }
+  char* base = static_cast<char*>(workspace);
+  fp.bar = reinterpret_cast<unsigned*>(base);
+  fp.flags = reinterpret_cast<unsigned*>(base + off_flags());
+  fp.rpart = reinterpret_cast<float*>(base + off_rpart());
+  fp.act = reinterpret_cast<float*>(base + off_act(d, B));
+  fp.act_stride = d->inter > d->shared_inter ? d->inter : d->shared_inter;
+  fp.out_idx = out_idx;
+  fp.out_w = out_w;
+  fp.trace = (d->flags & ZMOE_LAYER_TRACE) ? reinterpret_cast<unsigned long long*>(base + off_trace(d, B)) : nullptr;
+  const size_t lds = fused_lds_bytes(d, B);
+  if (d->quant_mode == ZMOE_Q_AFFINE) return launch_fused_t<ZMOE_Q_AFFINE>(st, fp, lds);
+  return launch_fused_t<ZMOE_Q_MXFP4>(st, fp, lds);
+}
+
+}  // namespace zmoe

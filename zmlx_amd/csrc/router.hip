@@ -1,0 +1,221 @@
+// Router kernels: dense router projection and the top-k gating variants.
+// One wave owns one token row for the top-k kernels; the selection order is
+// "higher value first, lower expert index on ties" (zmoe_wave.h).
+#include "zmoe_common.h"
+#include "zmoe_host.h"
+#include "zmoe_route.h"
+
+namespace zmoe {
+
+constexpr int kRouterMaxE = 1024;
+constexpr int kRouterMaxK = kMaxTopK;
+
+// ---------------------------------------------------------------------------
+// Dense router projection: logits[b, e] = x[b, :] . w[e, :]
+// ---------------------------------------------------------------------------
+constexpr int kLogitTok = 4;   // tokens per block
+constexpr int kLogitRows = 2;  // rows per wave
+
+__global__ __launch_bounds__(256) void k_dense_logits(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                      int B, int E, int H, int out_f32, void* __restrict__ out) {
+  extern __shared__ __align__(16) uint32_t xsm[];  // kLogitTok * H bf16
+  const int b0 = blockIdx.y * kLogitTok;
+  const int nt = min(kLogitTok, B - b0);
+  const int hw = H >> 1;  // dwords per row
+  for (int i = threadIdx.x; i < nt * hw; i += blockDim.x) {
+    xsm[i] = reinterpret_cast<const uint32_t*>(x + static_cast<int64_t>(b0) * H)[i];
+  }
+  __syncthreads();
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int e0 = (blockIdx.x * 4 + wave) * kLogitRows;
+  if (e0 >= E) return;
+  float acc[kLogitRows][kLogitTok];
+#pragma unroll
+  for (int r = 0; r < kLogitRows; ++r)
+#pragma unroll
+    for (int t = 0; t < kLogitTok; ++t) acc[r][t] = 0.0f;
+
+  // chunks of 512 elements (8 per lane); each chunk's dot is reduced across
+  // the wave, then chunks are added in order -- the same order as the fused
+  // decode kernel, so both produce identical logits.
+  for (int c0 = 0; c0 < H; c0 += 512) {
+    const int h = c0 + lane * 8;
+    const bool valid = h < H;
+    uint4 wv[kLogitRows];
+#pragma unroll
+    for (int r = 0; r < kLogitRows; ++r) {
+      const int e = min(e0 + r, E - 1);
+      wv[r] = valid ? *reinterpret_cast<const uint4*>(w + static_cast<int64_t>(e) * H + h) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int t = 0; t < kLogitTok; ++t) {
+      if (t < nt) {
+        const uint4 xv = valid ? *reinterpret_cast<const uint4*>(xsm + t * hw + (h >> 1)) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < kLogitRows; ++r) {
+          float a = 0.0f;
+          a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv[r].x), __builtin_bit_cast(bf16x2_t, xv.x), a, false);
+          a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv[r].y), __builtin_bit_cast(bf16x2_t, xv.y), a, false);
+          a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv[r].z), __builtin_bit_cast(bf16x2_t, xv.z), a, false);
+          a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv[r].w), __builtin_bit_cast(bf16x2_t, xv.w), a, false);
+          acc[r][t] += wave_sum(a);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kLogitRows; ++r) {
+#pragma unroll
+    for (int t = 0; t < kLogitTok; ++t) {
+      const float v = acc[r][t];
+      if (lane == 0 && t < nt && e0 + r < E) {
+        const int64_t o = static_cast<int64_t>(b0 + t) * E + e0 + r;
+        if (out_f32)
+          static_cast<float*>(out)[o] = v;
+        else
+          static_cast<uint16_t*>(out)[o] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Top-k gating kernels: one wave per token row (4 rows per block); the row is
+// staged in wave-private LDS and routed by route_row (zmoe_route.h), the same
+// code the single-launch layer kernel runs.
+// ---------------------------------------------------------------------------
+struct RouterBlockLds {
+  float v[4][kRouterMaxE];
+  float aff[4][kRouterMaxE];
+  RouteLds r[4];
+};
+
+__global__ __launch_bounds__(256) void k_route_rows(const void* __restrict__ logits, int dtype, int B, RouteArgs a,
+                                                    int out_bf16, void* __restrict__ out_w,
+                                                    uint32_t* __restrict__ out_idx) {
+  __shared__ RouterBlockLds S;
+  const int wave = threadIdx.x / kWave;
+  const int row = blockIdx.x * 4 + wave;
+  if (row >= B) return;  // wave-private LDS only: no block barriers
+  const int lane = __lane_id();
+  float* v = S.v[wave];
+  for (int e = lane; e < a.E; e += kWave) {
+    const int64_t i = static_cast<int64_t>(row) * a.E + e;
+    v[e] = (dtype == ZMOE_DT_F32) ? static_cast<const float*>(logits)[i]
+                                  : bf16_bits_to_f32(static_cast<const uint16_t*>(logits)[i]);
+  }
+  wave_lds_sync();
+  route_row(a, v, S.aff[wave], S.r[wave]);
+  if (lane < a.k) {
+    const int64_t o = static_cast<int64_t>(row) * a.k + lane;
+    const float w = S.r[wave].w[lane];
+    if (out_bf16)
+      static_cast<uint16_t*>(out_w)[o] = static_cast<uint16_t>(f32_to_bf16_bits(w));
+    else
+      static_cast<float*>(out_w)[o] = w;
+    out_idx[o] = static_cast<uint32_t>(S.r[wave].sel[lane]);
+  }
+}
+
+static int launch_route(hipStream_t st, const void* logits, int dtype, int B, const RouteArgs& a, int out_bf16,
+                        void* out_w, uint32_t* out_idx, const char* what) {
+  hipLaunchKernelGGL(k_route_rows, dim3((B + 3) / 4), dim3(256), 0, st, logits, dtype, B, a, out_bf16, out_w,
+                     out_idx);
+  return check_launch(what);
+}
+
+static RouteArgs make_args(int kind, int E, int k, int norm, const float* bias, int n_group, int topk_group,
+                           float scale, int w_bf16) {
+  RouteArgs a;
+  a.kind = kind;
+  a.E = E;
+  a.k = k;
+  a.norm = norm;
+  a.bias = bias;
+  a.n_group = n_group;
+  a.topk_group = topk_group;
+  a.scale = scale;
+  a.w_bf16 = w_bf16;
+  return a;
+}
+
+static int check_router(const char* op, int B, int E, int k) {
+  const std::string tag = std::string("[") + op + "] ";
+  ZMOE_REQUIRE(B >= 0 && E >= 1 && E <= kRouterMaxE, ZMOE_EINVAL_SHAPE, tag + "need 1 <= E <= 1024.");
+  ZMOE_REQUIRE(k >= 1, ZMOE_EINVAL_SHAPE, tag + "k must be > 0");
+  ZMOE_REQUIRE(k <= E, ZMOE_EINVAL_SHAPE, tag + "k=" + std::to_string(k) + " exceeds last dimension D=" + std::to_string(E));
+  ZMOE_REQUIRE(k <= kRouterMaxK, ZMOE_EUNSUPPORTED, tag + "k must be <= 16.");
+  return ZMOE_OK;
+}
+
+// Internal launchers for the layer composition (arguments pre-validated).
+int launch_topk_gating(hipStream_t st, const void* logits, int in_dtype, int B, int E, int k, const float* bias,
+                       int norm, int out_bf16, void* out_w, uint32_t* out_idx) {
+  return launch_route(st, logits, in_dtype, B, make_args(kRouteTopkLogits, E, k, norm, bias, 1, 1, 1.0f, out_bf16),
+                      out_bf16, out_w, out_idx, "topk_gating_softmax");
+}
+
+int launch_deepseek_router(hipStream_t st, const void* logits, int in_dtype, const float* bias, int B, int E, int k,
+                           int n_group, int topk_group, float scaling, float* out_w, uint32_t* out_idx) {
+  return launch_route(st, logits, in_dtype, B,
+                      make_args(kRouteSigmoidGrouped, E, k, 1, bias, n_group, topk_group, scaling, 0), 0, out_w,
+                      out_idx, "deepseek_router_topk_sigmoid");
+}
+
+}  // namespace zmoe
+
+using namespace zmoe;
+
+extern "C" int zmoe_dense_logits(void* stream, const void* x, const void* w, int B, int E, int H, int out_dtype,
+                                 void* out) {
+  ZMOE_REQUIRE(B >= 0 && E >= 1 && H >= 8 && H % 8 == 0, ZMOE_EINVAL_SHAPE, "[dense_logits] need H % 8 == 0.");
+  ZMOE_REQUIRE(out_dtype == ZMOE_DT_BF16 || out_dtype == ZMOE_DT_F32, ZMOE_EINVAL_DTYPE,
+               "[dense_logits] out dtype must be bf16 or f32.");
+  ZMOE_REQUIRE(static_cast<int64_t>(kLogitTok) * H * 2 <= 64 * 1024, ZMOE_EUNSUPPORTED, "[dense_logits] H too large.");
+  if (B == 0) return ZMOE_OK;
+  ZMOE_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0,
+               ZMOE_EINVAL_SHAPE, "[dense_logits] x and w must be 16-byte aligned.");
+  dim3 grid((E + 4 * kLogitRows - 1) / (4 * kLogitRows), (B + kLogitTok - 1) / kLogitTok);
+  hipLaunchKernelGGL(k_dense_logits, grid, dim3(256), static_cast<size_t>(kLogitTok) * H * 2, as_stream(stream),
+                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), B, E, H,
+                     out_dtype == ZMOE_DT_F32 ? 1 : 0, out);
+  return check_launch("dense_logits");
+}
+
+extern "C" int zmoe_router_softmax_topk(void* stream, const void* logits, int B, int E, int k, int norm_topk_prob,
+                                        void* out_w, uint32_t* out_idx) {
+  int rc = check_router("router_softmax_topk", B, E, k);
+  if (rc) return rc;
+  if (B == 0) return ZMOE_OK;
+  return launch_route(as_stream(stream), logits, ZMOE_DT_BF16, B,
+                      make_args(kRouteSoftmaxProbs, E, k, norm_topk_prob ? 1 : 0, nullptr, 1, 1, 1.0f, 1), 1, out_w,
+                      out_idx, "router_softmax_topk");
+}
+
+extern "C" int zmoe_topk_gating_softmax(void* stream, const void* logits, int in_dtype, int B, int E, int k,
+                                        const float* expert_bias, int norm_topk_prob, float* out_w,
+                                        uint32_t* out_idx) {
+  int rc = check_router("topk_gating_softmax", B, E, k);
+  if (rc) return rc;
+  ZMOE_REQUIRE(in_dtype == ZMOE_DT_BF16 || in_dtype == ZMOE_DT_F32, ZMOE_EINVAL_DTYPE,
+               "[topk_gating_softmax] logits must be bf16 or f32.");
+  if (B == 0) return ZMOE_OK;
+  return launch_topk_gating(as_stream(stream), logits, in_dtype, B, E, k, expert_bias, norm_topk_prob ? 1 : 0, 0,
+                            out_w, out_idx);
+}
+
+extern "C" int zmoe_deepseek_router_topk_sigmoid(void* stream, const float* logits, const float* bias, int B, int E,
+                                                 int k, int n_group, int topk_group, float routed_scaling_factor,
+                                                 float* out_w, uint32_t* out_idx) {
+  int rc = check_router("deepseek_router_topk_sigmoid", B, E, k);
+  if (rc) return rc;
+  ZMOE_REQUIRE(n_group > 0, ZMOE_EINVAL_SHAPE, "[deepseek_router_topk_sigmoid] n_group must be > 0");
+  ZMOE_REQUIRE(topk_group > 0 && topk_group <= n_group, ZMOE_EINVAL_SHAPE,
+               "[deepseek_router_topk_sigmoid] invalid topk_group");
+  ZMOE_REQUIRE(E % n_group == 0, ZMOE_EINVAL_SHAPE, "[deepseek_router_topk_sigmoid] n_group must divide D");
+  ZMOE_REQUIRE(n_group <= kWave, ZMOE_EUNSUPPORTED, "[deepseek_router_topk_sigmoid] n_group must be <= 64");
+  ZMOE_REQUIRE(bias != nullptr, ZMOE_EINVAL_SHAPE, "[deepseek_router_topk_sigmoid] bias must have shape (D,)");
+  if (B == 0) return ZMOE_OK;
+  return launch_deepseek_router(as_stream(stream), logits, ZMOE_DT_F32, bias, B, E, k, n_group, topk_group,
+                                routed_scaling_factor, out_w, out_idx);
+}
