@@ -214,9 +214,12 @@ typedef struct zmoe_layer_desc {
 size_t zmoe_moe_layer_trace_info(const zmoe_layer_desc* desc, int B, int* n_blocks, int* n_slots);
 
 /* Bytes of device workspace zmoe_moe_layer needs for B tokens.  The first
- * 256 bytes hold the fused kernel's grid-barrier counters: the workspace must
- * be zero-filled once before its first use; every call leaves them zero again
- * (bytes 128..131 hold a sticky error word: nonzero if a barrier wait timed out). */
+ * 16 KiB hold the single-launch kernel's grid-barrier state (arrival
+ * counters and per-workgroup generation numbers that only ever increase):
+ * the workspace must be zero-filled once before its first use and that
+ * block must not be written by anything else afterwards.  Bytes 128..131
+ * hold a sticky error word: nonzero if a barrier wait timed out (the block
+ * is then inconsistent; zero-fill the workspace again before reuse). */
 size_t zmoe_moe_layer_workspace_size(const zmoe_layer_desc* desc, int B);
 
 /*

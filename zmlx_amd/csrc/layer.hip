@@ -96,7 +96,7 @@ extern "C" size_t zmoe_moe_layer_workspace_size(const zmoe_layer_desc* desc, int
   if (!desc || B < 0) return 0;
   const size_t multi = layout_ws(desc, B, nullptr).bytes;
   const size_t fused = fused_supported(desc, B) ? fused_workspace_bytes(desc, B) : 0;
-  return 256 + (multi > fused ? multi : fused);
+  return (kSyncBlockBytes + multi > fused) ? kSyncBlockBytes + multi : fused;
 }
 
 extern "C" size_t zmoe_moe_layer_trace_info(const zmoe_layer_desc* desc, int B, int* n_blocks, int* n_slots) {
@@ -115,8 +115,8 @@ extern "C" int zmoe_moe_layer(void* stream, const zmoe_layer_desc* d, const void
   if (use_fused(d, B)) {
     return launch_fused(as_stream(stream), d, x, B, out, out_idx, out_w, workspace);
   }
-  // multi-kernel sequence: its buffers start after the 256-byte sync block
-  LayerWs ws = layout_ws(d, B, static_cast<char*>(workspace) + 256);
+  // multi-kernel sequence: its buffers start after the barrier-state block
+  LayerWs ws = layout_ws(d, B, static_cast<char*>(workspace) + kSyncBlockBytes);
   ZMOE_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(workspace) & 255) == 0,
                ZMOE_EINVAL_SHAPE, "[moe_layer] x must be 16-byte and workspace 256-byte aligned.");
   hipStream_t st = as_stream(stream);

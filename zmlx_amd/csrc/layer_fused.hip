@@ -25,11 +25,18 @@
 // written with rolled loops (per-token accumulators live in LDS) to stay
 // within the instruction cache.  Cross-workgroup data (router partials,
 // act rows, barrier words) use device-scope atomic accesses, which are
-// coherent across the XCDs without cache-wide writeback/invalidate.  A
-// barrier: every workgroup bumps one counter; the last arrival resets it and
-// raises one flag per workgroup (own 128-byte line, so no polling hot spot).
-// Every wait is bounded (on timeout: sticky error word, continue), so the
-// grid always drains.  The arithmetic is the multi-kernel path's (same dot
+// coherent across the XCDs without cache-wide writeback/invalidate.
+//
+// Grid barrier: workgroup g adds 1 (no return value) to arrival counter
+// g % 32, spreading same-address atomics over 32 lines; wave 0 of
+// workgroup 0 polls the 32 counters and then writes the generation number
+// to 8 release words, which the workgroups poll (g % 8).  Counters and
+// generations only increase (generation = 2 x launches so far + barrier
+// index, each workgroup keeps its launch count), so nothing is reset.
+// Waves wait only for their own stores before arriving and order LDS-only
+// within the workgroup, so weight prefetches stay in flight across a
+// barrier.  Every wait is bounded (on timeout: sticky error word,
+// continue), so the grid always drains.  The arithmetic is the multi-kernel path's (same dot
 // products, reduction trees, routing code and combine): results are
 // bit-identical to it.
 #include "zmoe_common.h"
@@ -47,7 +54,16 @@ constexpr int kChunkA = 4;                // (row-group, segment) items per batc
 constexpr int kChunkD = 8;                // (slot-group, segment) items per batch, phase D
 constexpr unsigned kSpinLimit = 1u << 21;
 constexpr int kTraceSlots = 16;
-constexpr int kFlagStride = 32;           // uint32 words between barrier flags (128 B)
+constexpr int kBarCtrs = 32;              // arrival counters
+constexpr int kBarRel = 8;                // release words
+constexpr int kLineWords = 32;            // 128-byte line, in uint32 words
+// barrier-state words at the start of the workspace
+constexpr int kErrWord = static_cast<int>(kSyncErrorByte / 4);
+constexpr int kCtrWord = 64;
+constexpr int kRelWord = kCtrWord + kBarCtrs * kLineWords;
+constexpr int kEpochWord = kRelWord + kBarRel * kLineWords;  // + workgroup
+constexpr int kMaxGrid = static_cast<int>(kSyncBlockBytes / 4) - kEpochWord;
+constexpr int kMaxNC = 16;                // router chunks of 512 (H <= 8192)
 
 struct FusedParams {
   int H, E, K, I, Is, B;
@@ -60,10 +76,9 @@ struct FusedParams {
   const uint32_t* w[6];  // gate, up, down, sh_gate, sh_up, sh_down
   const void* s[6];
   const void* b[6];
-  unsigned* bar;         // [0] counter 1, [16] counter 2, [32] error word
-  unsigned* flags;       // [2][G][kFlagStride]
+  unsigned* sync;        // barrier-state block (words kErrWord, kCtrWord, ...)
   float* rpart;          // [B][E][NC]
-  float* act;            // [B*K + B][act_stride] (bf16 values held in f32)
+  uint16_t* act;         // [B*K + B][act_stride] bf16
   int act_stride;
   uint32_t* out_idx;
   float* out_w;
@@ -80,126 +95,109 @@ struct FusedLds {
 };
 
 __device__ __forceinline__ void trace_mark(const FusedParams& p, int slot) {
-  if (p.trace && threadIdx.x == 0) p.trace[blockIdx.x * kTraceSlots + slot] = wall_clock64();
+  if (p.trace && threadIdx.x == 0) gstore(p.trace + blockIdx.x * kTraceSlots + slot, static_cast<unsigned long long>(wall_clock64()));
 }
 
-__device__ __forceinline__ void dev_store(float* a, float v) {
-  __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Arrival at a grid barrier.  Precondition: every wave of the workgroup
+// has waited for its own device-scope stores and then passed lds_barrier().
+__device__ __forceinline__ void bar_arrive(const FusedParams& p) {
+  if (threadIdx.x == 0)
+    (void)__hip_atomic_fetch_add((ZMOE_GLOBAL unsigned*)(p.sync + kCtrWord + (blockIdx.x % kBarCtrs) * kLineWords),
+                                 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ float dev_load(const float* a) {
-  return __hip_atomic_load(const_cast<float*>(a), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void bar_timeout(const FusedParams& p) {
+  __hip_atomic_fetch_or((ZMOE_GLOBAL unsigned*)(p.sync + kErrWord), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ void grid_sync(const FusedParams& p, int which) {
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's device-scope stores are performed
-  __syncthreads();
-  if (threadIdx.x < kWave) {
+// Wait for generation `gen` (every workgroup arrived `gen` times in total).
+__device__ void bar_wait(const FusedParams& p, unsigned gen) {
+  if (blockIdx.x == 0 && threadIdx.x < kWave) {
     const unsigned G = gridDim.x;
-    unsigned* cnt = p.bar + 16 * which;
-    unsigned* fl = p.flags + static_cast<size_t>(which) * G * kFlagStride;
-    int last = 0;
-    if (threadIdx.x == 0) last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1;
-    last = __shfl(last, 0);
-    if (last) {
-      if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      for (unsigned i = threadIdx.x; i < G; i += kWave)
-        __hip_atomic_store(fl + static_cast<size_t>(i) * kFlagStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (threadIdx.x == 0) {
-      unsigned* mine = fl + static_cast<size_t>(blockIdx.x) * kFlagStride;
-      unsigned n = 0;
-      while (__hip_atomic_load(mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
-        if (++n > kSpinLimit) {
-          __hip_atomic_fetch_or(p.bar + 32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
+    const unsigned c = threadIdx.x;
+    const unsigned per = c < kBarCtrs ? G / kBarCtrs + (c < G % kBarCtrs ? 1u : 0u) : 0u;
+    const unsigned target = gen * per;  // modulo 2^32, compared by difference
+    unsigned n = 0;
+    for (;;) {
+      const bool ok = c >= kBarCtrs || static_cast<int>(dev_load(p.sync + kCtrWord + c * kLineWords) - target) >= 0;
+      if (__all(ok)) break;
+      if (++n > kSpinLimit) {
+        if (c == 0) bar_timeout(p);
+        break;
       }
-      __hip_atomic_store(mine, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    if (c < kBarRel) dev_store(p.sync + kRelWord + c * kLineWords, gen);
   }
-  __syncthreads();
-}
-
-// Cross-lane sum over aligned groups of L lanes (L a power of two <= 64);
-// same butterfly order as wave_sum_width<L>.
-__device__ __forceinline__ float lanes_sum(float v, int L) {
-  for (int o = L >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
-// x rows (bf16) -> LDS tile in the layout of qmv.hip (stage_x_row).
-template <int QMODE>
-__device__ void stage_rows_lds(const uint16_t* __restrict__ src, int64_t src_stride, int nrows, int S, uint32_t* xs,
-                               float* sx) {
-  for (int i = threadIdx.x; i < nrows * S * 4; i += blockDim.x) {
-    const int r = i / (S * 4);
-    const int rem = i - r * S * 4;
-    const int s = rem >> 2, j = rem & 3;
-    const uint4 v = *reinterpret_cast<const uint4*>(src + r * src_stride + s * 32 + j * 8);
-    uint4 o;
-    if (QMODE == ZMOE_Q_AFFINE) {
-      o.x = (v.x & 0xFFFFu) | (v.z << 16);
-      o.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
-      o.z = (v.y & 0xFFFFu) | (v.w << 16);
-      o.w = (v.y >> 16) | (v.w & 0xFFFF0000u);
-    } else {
-      o = v;
-    }
-    *reinterpret_cast<uint4*>(xs + ((r * 4 + j) * S + s) * 4) = o;
-  }
-  if (QMODE == ZMOE_Q_AFFINE) {
-    for (int i = threadIdx.x; i < nrows * S; i += blockDim.x) {
-      const int r = i / S, s = i - r * S;
-      const uint4* q = reinterpret_cast<const uint4*>(src + r * src_stride + s * 32);
-      float acc = 0.0f;
-      for (int w = 0; w < 4; ++w) {
-        const uint4 v = q[w];
-        acc += bf16_bits_to_f32(v.x & 0xFFFFu) + bf16_bits_to_f32(v.x >> 16);
-        acc += bf16_bits_to_f32(v.y & 0xFFFFu) + bf16_bits_to_f32(v.y >> 16);
-        acc += bf16_bits_to_f32(v.z & 0xFFFFu) + bf16_bits_to_f32(v.z >> 16);
-        acc += bf16_bits_to_f32(v.w & 0xFFFFu) + bf16_bits_to_f32(v.w >> 16);
+  if (threadIdx.x == 0) {
+    const unsigned* rel = p.sync + kRelWord + (blockIdx.x % kBarRel) * kLineWords;
+    unsigned n = 0;
+    while (static_cast<int>(dev_load(rel) - gen) < 0) {
+      if (++n > kSpinLimit) {
+        bar_timeout(p);
+        break;
       }
-      sx[r * S + s] = acc;
     }
   }
+  lds_barrier();
 }
 
-// act rows (f32 holding bf16 values, device-coherent loads) -> same layout.
-template <int QMODE>
-__device__ void stage_act_lds(const float* __restrict__ src, int64_t src_stride, int nrows, int S, uint32_t* xs,
-                              float* sx) {
-  for (int i = threadIdx.x; i < nrows * S * 4; i += blockDim.x) {
-    const int r = i / (S * 4);
-    const int rem = i - r * S * 4;
-    const int s = rem >> 2, j = rem & 3;
-    const float* q = src + r * src_stride + s * 32 + j * 8;
-    uint32_t e[8];
+// bf16 rows -> LDS tile in the layout of qmv.hip (stage_x_row):
+//   xs[((r*4 + j)*S + s)*4 + d], sums sx[r*S + s] (affine).
+// DEV: read the rows with device-coherent 64-bit loads (rows written by
+// other workgroups in this launch).
+template <int QMODE, bool DEV>
+__device__ __forceinline__ void stage_rows_lds(const uint16_t* __restrict__ src, int64_t src_stride, int nrows, int S,
+                                               uint32_t* xs, float* sx) {
+  // all (row, segment, quarter) items at once, two per thread per round, so
+  // the loads of every row are in flight together
+  const int S4 = S * 4;
+  const int n = nrows * S4;
+  for (int i0 = threadIdx.x; i0 < n; i0 += 2 * kFThreads) {
+    uint4 v[2];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) e[t] = __float_as_uint(dev_load(q + t)) >> 16;
-    uint4 o;
-    if (QMODE == ZMOE_Q_AFFINE) {
-      o.x = e[0] | (e[4] << 16);
-      o.y = e[1] | (e[5] << 16);
-      o.z = e[2] | (e[6] << 16);
-      o.w = e[3] | (e[7] << 16);
-    } else {
-      o.x = e[0] | (e[1] << 16);
-      o.y = e[2] | (e[3] << 16);
-      o.z = e[4] | (e[5] << 16);
-      o.w = e[6] | (e[7] << 16);
+    for (int h = 0; h < 2; ++h) {
+      const int i = i0 + h * kFThreads;
+      if (i < n) {
+        const int r = i / S4, rem = i - r * S4;
+        const uint16_t* q16 = src + r * src_stride + rem * 8;  // segment rem>>2, quarter rem&3
+        if (DEV) {
+          const unsigned long long* q = reinterpret_cast<const unsigned long long*>(q16);
+          const unsigned long long lo = dev_load(q);
+          const unsigned long long hi = dev_load(q + 1);
+          v[h] = make_uint4(static_cast<uint32_t>(lo), static_cast<uint32_t>(lo >> 32), static_cast<uint32_t>(hi),
+                            static_cast<uint32_t>(hi >> 32));
+        } else {
+          v[h] = gload(reinterpret_cast<const uint4*>(q16));
+        }
+      }
     }
-    *reinterpret_cast<uint4*>(xs + ((r * 4 + j) * S + s) * 4) = o;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int i = i0 + h * kFThreads;
+      if (i < n) {
+        const int r = i / S4, rem = i - r * S4;
+        const int s = rem >> 2, j = rem & 3;
+        uint4 o;
+        if (QMODE == ZMOE_Q_AFFINE) {
+          o.x = (v[h].x & 0xFFFFu) | (v[h].z << 16);
+          o.y = (v[h].x >> 16) | (v[h].z & 0xFFFF0000u);
+          o.z = (v[h].y & 0xFFFFu) | (v[h].w << 16);
+          o.w = (v[h].y >> 16) | (v[h].w & 0xFFFF0000u);
+        } else {
+          o = v[h];
+        }
+        *reinterpret_cast<uint4*>(xs + ((r * 4 + j) * S + s) * 4) = o;
+      }
+    }
   }
   if (QMODE == ZMOE_Q_AFFINE) {
-    __syncthreads();
-    for (int i = threadIdx.x; i < nrows * S; i += blockDim.x) {
+    lds_barrier();
+    for (int i = threadIdx.x; i < nrows * S; i += kFThreads) {
       const int r = i / S, s = i - r * S;
       float acc = 0.0f;
       for (int w = 0; w < 4; ++w) {
-        // pairs (e0,e4) (e1,e5) (e2,e6) (e3,e7); summed as in stage_x_row:
-        // (e0+e1) (e2+e3) (e4+e5) (e6+e7)
+        // pairs (e0,e4) (e1,e5) (e2,e6) (e3,e7) summed in natural order:
+        // (e0+e1) (e2+e3) (e4+e5) (e6+e7), as stage_x_row does
         const uint4 o = *reinterpret_cast<const uint4*>(xs + ((r * 4 + w) * S + s) * 4);
         acc += bf16_bits_to_f32(o.x & 0xFFFFu) + bf16_bits_to_f32(o.y & 0xFFFFu);
         acc += bf16_bits_to_f32(o.z & 0xFFFFu) + bf16_bits_to_f32(o.w & 0xFFFFu);
@@ -236,14 +234,33 @@ __device__ __forceinline__ float seg_dot_lds(const uint4 w, const uint32_t* xs, 
   return v;
 }
 
+// Quantisation parameters of one (row, segment): loaded raw, decoded at use
+// (decoding right after the load would make the load's wait immediate).
+struct RawParam {
+  uint32_t s, b;
+};
+
 template <int QMODE>
-__device__ __forceinline__ void seg_param(const void* __restrict__ scales, const void* __restrict__ biases, int64_t idx,
-                                          float& s, float& c) {
+__device__ __forceinline__ RawParam seg_param_load(const void* __restrict__ scales, const void* __restrict__ biases,
+                                                   int64_t idx) {
+  RawParam r;
   if (QMODE == ZMOE_Q_AFFINE) {
-    s = bf16_bits_to_f32(static_cast<const uint16_t*>(scales)[idx]);
-    c = bf16_bits_to_f32(static_cast<const uint16_t*>(biases)[idx]) - 128.0f * s;
+    r.s = gload(static_cast<const uint16_t*>(scales) + idx);
+    r.b = gload(static_cast<const uint16_t*>(biases) + idx);
   } else {
-    s = e8m0_to_f32(static_cast<const uint8_t*>(scales)[idx]);
+    r.s = gload(static_cast<const uint8_t*>(scales) + idx);
+    r.b = 0;
+  }
+  return r;
+}
+
+template <int QMODE>
+__device__ __forceinline__ void seg_param_decode(RawParam r, float& s, float& c) {
+  if (QMODE == ZMOE_Q_AFFINE) {
+    s = bf16_bits_to_f32(r.s);
+    c = bf16_bits_to_f32(r.b) - 128.0f * s;
+  } else {
+    s = e8m0_to_f32(r.s);
     c = 0.0f;
   }
 }
@@ -276,7 +293,7 @@ __device__ __forceinline__ UnitPtr unit_ptr(const FusedParams& p, const FusedLds
   return r;
 }
 
-template <int QMODE>
+template <int QMODE, int P>
 __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   FusedLds& L = *reinterpret_cast<FusedLds*>(smem);
@@ -293,21 +310,22 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
   const int S_H = p.H >> 5, S_I = p.I >> 5;
   const bool has_shared = p.Is > 0;
   trace_mark(p, 0);
-  if (p.trace && threadIdx.x == 0) p.trace[blockIdx.x * kTraceSlots + 13] = clock64();
+  if (p.trace && threadIdx.x == 0) gstore(p.trace + blockIdx.x * kTraceSlots + 13, static_cast<unsigned long long>(clock64()));
+  // launches this workgroup completed before (written by itself only)
+  const unsigned epoch = wave == 0 ? dev_load(p.sync + kEpochWord + blockIdx.x) : 0u;
 
-  // phase R..A LDS: x tile, x sums, router rows, phase-A accumulators
+  // phase R..A LDS: x tile, x sums, grouped-router scratch, accumulators
   uint32_t* xs = reinterpret_cast<uint32_t*>(big);
   float* sx = reinterpret_cast<float*>(xs + static_cast<size_t>(B) * S_H * 16);
-  float* rv = sx + static_cast<size_t>(B) * S_H;          // [B][E]
-  float* raff = rv + static_cast<size_t>(B) * E;          // [B][E]
-  float* accA = raff + static_cast<size_t>(B) * E;        // [waves][2][B][64]
+  float* rv = sx + static_cast<size_t>(B) * S_H;    // [B][E]
+  float* accA = rv + static_cast<size_t>(B) * E;    // [waves][2][B][64]
 
   // ---------------- phase R: router partials ----------------
   for (int u = gw; u < E * NC; u += W) {
     const int e = u / NC, c = u - e * NC;
-    const uint4 wv = *reinterpret_cast<const uint4*>(p.wr + static_cast<int64_t>(e) * p.H + c * 512 + lane * 8);
+    const uint4 wv = gload(reinterpret_cast<const uint4*>(p.wr + static_cast<int64_t>(e) * p.H + c * 512 + lane * 8));
     for (int b = 0; b < B; ++b) {
-      const uint4 xv = *reinterpret_cast<const uint4*>(p.x + static_cast<int64_t>(b) * p.H + c * 512 + lane * 8);
+      const uint4 xv = gload(reinterpret_cast<const uint4*>(p.x + static_cast<int64_t>(b) * p.H + c * 512 + lane * 8));
       float a = 0.0f;
       a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv.x), __builtin_bit_cast(bf16x2_t, xv.x), a, false);
       a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv.y), __builtin_bit_cast(bf16x2_t, xv.y), a, false);
@@ -317,34 +335,44 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
       if (lane == 0) dev_store(p.rpart + (static_cast<int64_t>(b) * E + e) * NC + c, a);
     }
   }
-  stage_rows_lds<QMODE>(p.x, p.H, B, S_H, xs, sx);
+  stage_rows_lds<QMODE, false>(p.x, p.H, B, S_H, xs, sx);
   trace_mark(p, 1);
-  grid_sync(p, 0);
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's partials are stored
+  lds_barrier();
+  bar_arrive(p);
+  bar_wait(p, 2 * epoch + 1);
   trace_mark(p, 2);
 
   // ---------------- phase T: routing (wave b <-> token b) ----------------
   if (wave < B) {
     const int b = wave;
-    float* v = rv + static_cast<size_t>(b) * E;
     const float* rp = p.rpart + static_cast<int64_t>(b) * E * NC;
-    for (int e = lane; e < E; e += kWave) {
-      float a = 0.0f;
-      for (int c = 0; c < NC; ++c) a += dev_load(rp + e * NC + c);  // chunks in order
-      v[e] = round_bf16(a);  // the gate Linear returns bf16 logits
-    }
-    wave_lds_sync();
     trace_mark(p, 3);
-    route_row(p.route, v, raff + static_cast<size_t>(b) * E, L.route[b]);
+    route_row_p<P>(
+        p.route,
+        [&](int e) {
+          float part[kMaxNC];
+#pragma unroll
+          for (int c = 0; c < kMaxNC; ++c)
+            if (c < NC) part[c] = dev_load(rp + e * NC + c);
+          float a = 0.0f;
+#pragma unroll
+          for (int c = 0; c < kMaxNC; ++c)
+            if (c < NC) a += part[c];  // chunks in order
+          return round_bf16(a);        // the gate Linear returns bf16 logits
+        },
+        *(ZMOE_LDS RouteLds*)(&L.route[b]), (ZMOE_LDS float*)(rv + static_cast<size_t>(b) * E));
     trace_mark(p, 4);
     if (blockIdx.x == 0 && lane < p.K) {
-      if (p.out_idx) p.out_idx[b * p.K + lane] = static_cast<uint32_t>(L.route[b].sel[lane]);
-      if (p.out_w) p.out_w[b * p.K + lane] = L.route[b].w[lane];
+      if (p.out_idx) gstore(p.out_idx + b * p.K + lane, static_cast<uint32_t>(L.route[b].sel[lane]));
+      if (p.out_w) gstore(p.out_w + b * p.K + lane, L.route[b].w[lane]);
     }
   }
   for (int e = threadIdx.x; e < E; e += blockDim.x) L.slot_of[e] = -1;
   __syncthreads();
-  const int npairs = B * p.K;
-  for (int q = threadIdx.x; q < npairs; q += blockDim.x) L.slot_of[L.route[q / p.K].sel[q % p.K]] = 0;
+  const int K = p.K;
+  const int npairs = B * K;
+  if (threadIdx.x < npairs) L.slot_of[L.route[threadIdx.x / K].sel[threadIdx.x % K]] = 0;
   __syncthreads();
   if (wave == 0) {  // unit slots in expert order
     int base = 0;
@@ -366,8 +394,9 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
     }
   }
   __syncthreads();
-  for (int q = threadIdx.x; q < npairs; q += blockDim.x) {
-    const int u = L.slot_of[L.route[q / p.K].sel[q % p.K]];
+  if (threadIdx.x < npairs) {
+    const int q = threadIdx.x;
+    const int u = L.slot_of[L.route[q / K].sel[q % K]];
     L.upairs[u][atomicAdd(&L.ucount[u], 1)] = q;
   }
   if (has_shared && threadIdx.x < B) L.upairs[L.nunits][threadIdx.x] = npairs + threadIdx.x;
@@ -379,67 +408,75 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
   // ---------------- phase A: gate/up + SwiGLU ----------------
   {
     const int LH = p.LH, RPI = kWave / LH;
-    const int rs = lane / LH, li = lane % LH;
+    const int rs = lane / LH, li = lane & (LH - 1);
     const int T = S_H / LH;
-    const int rg_routed = p.I / RPI;
-    const int rg_total = U * rg_routed + (has_shared ? p.Is / RPI : 0);
+    const int rgu = p.I / RPI;  // row-groups per unit (Is == I)
+    const int rg_total = Uall * rgu;
     const int per = (rg_total + W - 1) / W;
-    const int g0 = gw * per, g1 = min(rg_total, g0 + per);
-    const int n_items = max(0, g1 - g0) * T;
+    const int g0 = min(rg_total, gw * per), g1 = min(rg_total, g0 + per);
+    const int n_items = (g1 - g0) * T;
     const int64_t wpr = p.H >> 3;
     const int64_t ppr = (QMODE == ZMOE_Q_AFFINE) ? (S_H >> p.gshift) : S_H;
     float* ag = accA + (static_cast<size_t>(wave) * 2 * B) * kWave + lane;  // [tk] stride 64
     float* au = ag + static_cast<size_t>(B) * kWave;
+    // wave-uniform cursor over (unit, row-group, segment)
+    int cu_unit = g0 / max(rgu, 1);
+    int cu_rg = g0 - cu_unit * rgu;
+    int cu_t = 0;
     for (int base = 0; base < n_items; base += kChunkA) {
       uint4 wg[kChunkA], wu[kChunkA];
-      float sg[kChunkA], cg[kChunkA], su[kChunkA], cu[kChunkA];
+      RawParam rg[kChunkA], ru[kChunkA];
+      int iu[kChunkA], irow[kChunkA], it_[kChunkA];
 #pragma unroll
       for (int j = 0; j < kChunkA; ++j) {
-        const int it = base + j;
-        if (it < n_items) {
-          const int gi = it / T, t = it - gi * T;
-          const int g = g0 + gi;
-          const int u = g < U * rg_routed ? g / rg_routed : U;
-          const int row = (g - (u < U ? u * rg_routed : U * rg_routed)) * RPI + rs;
-          const int s = t * LH + li;
-          const UnitPtr pg = unit_ptr<QMODE>(p, L, u, 0);
-          const UnitPtr pu = unit_ptr<QMODE>(p, L, u, 1);
-          wg[j] = *reinterpret_cast<const uint4*>(pg.w + row * wpr + s * 4);
-          wu[j] = *reinterpret_cast<const uint4*>(pu.w + row * wpr + s * 4);
+        iu[j] = cu_unit;
+        irow[j] = cu_rg * RPI + rs;
+        it_[j] = cu_t;
+        if (base + j < n_items) {
+          const int s = cu_t * LH + li;
+          const UnitPtr pg = unit_ptr<QMODE>(p, L, cu_unit, 0);
+          const UnitPtr pu = unit_ptr<QMODE>(p, L, cu_unit, 1);
+          const int64_t row = irow[j];
+          wg[j] = gload(reinterpret_cast<const uint4*>(pg.w + row * wpr + s * 4));
+          wu[j] = gload(reinterpret_cast<const uint4*>(pu.w + row * wpr + s * 4));
           const int pi = (QMODE == ZMOE_Q_AFFINE) ? (s >> p.gshift) : s;
-          seg_param<QMODE>(pg.s, pg.b, row * ppr + pi, sg[j], cg[j]);
-          seg_param<QMODE>(pu.s, pu.b, row * ppr + pi, su[j], cu[j]);
+          rg[j] = seg_param_load<QMODE>(pg.s, pg.b, row * ppr + pi);
+          ru[j] = seg_param_load<QMODE>(pu.s, pu.b, row * ppr + pi);
+          if (++cu_t == T) {
+            cu_t = 0;
+            if (++cu_rg == rgu) {
+              cu_rg = 0;
+              ++cu_unit;
+            }
+          }
         }
       }
 #pragma unroll
       for (int j = 0; j < kChunkA; ++j) {
-        const int it = base + j;
-        if (it < n_items) {
-          const int gi = it / T, t = it - gi * T;
-          const int g = g0 + gi;
-          const int u = g < U * rg_routed ? g / rg_routed : U;
+        if (base + j < n_items) {
+          const int u = iu[j], t = it_[j];
           const int s = t * LH + li;
           const int nt = L.ucount[u];
+          float sgj, cgj, suj, cuj;
+          seg_param_decode<QMODE>(rg[j], sgj, cgj);
+          seg_param_decode<QMODE>(ru[j], suj, cuj);
           for (int tk = 0; tk < nt; ++tk) {
             const int q = L.upairs[u][tk];
-            const int b = (u < U) ? q / p.K : q - npairs;
+            const int b = (u < U) ? q / K : q - npairs;
             const float xsum = (QMODE == ZMOE_Q_AFFINE) ? sx[b * S_H + s] : 0.0f;
             const float g_prev = t == 0 ? 0.0f : ag[tk * kWave];
             const float u_prev = t == 0 ? 0.0f : au[tk * kWave];
-            ag[tk * kWave] = seg_accum<QMODE>(g_prev, sg[j], cg[j], seg_dot_lds<QMODE>(wg[j], xs, S_H, b, s), xsum);
-            au[tk * kWave] = seg_accum<QMODE>(u_prev, su[j], cu[j], seg_dot_lds<QMODE>(wu[j], xs, S_H, b, s), xsum);
+            ag[tk * kWave] = seg_accum<QMODE>(g_prev, sgj, cgj, seg_dot_lds<QMODE>(wg[j], xs, S_H, b, s), xsum);
+            au[tk * kWave] = seg_accum<QMODE>(u_prev, suj, cuj, seg_dot_lds<QMODE>(wu[j], xs, S_H, b, s), xsum);
           }
           if (base == 0 && j == 0) trace_mark(p, 6);
           if (t == T - 1) {  // row-group complete: reduce, SwiGLU, store act
-            const int row = (g - (u < U ? u * rg_routed : U * rg_routed)) * RPI + rs;
             for (int tk = 0; tk < nt; ++tk) {
               const float gv = lanes_sum(ag[tk * kWave], LH);
               const float uv = lanes_sum(au[tk * kWave], LH);
-              if (li == 0) {
-                const int q = L.upairs[u][tk];
-                dev_store(p.act + static_cast<int64_t>(q) * p.act_stride + row,
-                          bf16_bits_to_f32(swiglu_bf16(round_bf16(gv), round_bf16(uv))));
-              }
+              if (li == 0)
+                dev_store<uint16_t>(p.act + static_cast<int64_t>(L.upairs[u][tk]) * p.act_stride + irow[j],
+                              static_cast<uint16_t>(swiglu_bf16(round_bf16(gv), round_bf16(uv))));
             }
           }
         }
@@ -449,37 +486,57 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
   trace_mark(p, 7);
 
   // ---------------- phase D setup: first down batch before the barrier ----------------
+  // This wave owns output rows [h0, h0 + nrows); slot = (row, unit) with the
+  // unit fastest; RPID slots per load instruction, lane group rsD.
   const int LI = p.LI, RPID = kWave / LI;
-  const int rsD = lane / LI, liD = lane % LI;
+  const int rsD = lane / LI, liD = lane & (LI - 1);
   const int TD = S_I / LI;
   const int rows_per_wave = (p.H + W - 1) / W;
   const int h0 = gw * rows_per_wave;
   const int nrows = max(0, min(p.H, h0 + rows_per_wave) - h0);
-  const int slots = nrows * Uall;  // (h_local, unit), unit fastest
-  const int n_itemsD = ((slots + RPID - 1) / RPID) * TD;
+  const int slots = nrows * Uall;
+  const int n_groups = (slots + RPID - 1) / RPID;
+  const int n_itemsD = n_groups * TD;
   const int64_t wprD = p.I >> 3;
   const int64_t pprD = (QMODE == ZMOE_Q_AFFINE) ? (S_I >> p.gshift) : S_I;
+  // per-lane slot cursor (row hl, unit uu) and segment cursor (wave-uniform)
+  int d_hl = rsD / max(Uall, 1), d_u = rsD - d_hl * Uall, d_t = 0, d_g = 0;
   uint4 wd[kChunkD];
-  float sd[kChunkD], cd[kChunkD];
-#define ZMOE_LOAD_DOWN(BASE)                                                              \
-  _Pragma("unroll") for (int j = 0; j < kChunkD; ++j) {                                  \
-    const int it = (BASE) + j;                                                            \
-    if (it < n_itemsD) {                                                                  \
-      const int gi = it / TD, t = it - gi * TD;                                           \
-      const int slot = min(gi * RPID + rsD, slots - 1);                                   \
-      const int hl = slot / Uall, u = slot - hl * Uall;                                   \
-      const UnitPtr pd = unit_ptr<QMODE>(p, L, u, 2);                                     \
-      const int s = t * LI + liD;                                                         \
-      const int64_t row = h0 + hl;                                                        \
-      wd[j] = *reinterpret_cast<const uint4*>(pd.w + row * wprD + s * 4);                 \
-      const int pi = (QMODE == ZMOE_Q_AFFINE) ? (s >> p.gshift) : s;                      \
-      seg_param<QMODE>(pd.s, pd.b, row * pprD + pi, sd[j], cd[j]);                        \
-    }                                                                                     \
-  }
-  ZMOE_LOAD_DOWN(0)
+  RawParam rd[kChunkD];
+  int jhl[kChunkD], ju[kChunkD], jt[kChunkD], jvalid[kChunkD];
+  auto load_down_batch = [&](int base) {
+#pragma unroll
+    for (int j = 0; j < kChunkD; ++j) {
+      jhl[j] = min(d_hl, nrows - 1);
+      ju[j] = d_u;
+      jt[j] = d_t;
+      jvalid[j] = d_g * RPID + rsD < slots;
+      if (base + j < n_itemsD) {
+        const UnitPtr pd = unit_ptr<QMODE>(p, L, d_u, 2);
+        const int s = d_t * LI + liD;
+        const int64_t row = h0 + jhl[j];
+        wd[j] = gload(reinterpret_cast<const uint4*>(pd.w + row * wprD + s * 4));
+        const int pi = (QMODE == ZMOE_Q_AFFINE) ? (s >> p.gshift) : s;
+        rd[j] = seg_param_load<QMODE>(pd.s, pd.b, row * pprD + pi);
+        if (++d_t == TD) {  // next slot-group: advance this lane's slot by RPID
+          d_t = 0;
+          ++d_g;
+          d_u += RPID;
+          while (d_u >= Uall) {
+            d_u -= Uall;
+            ++d_hl;
+          }
+          d_u = (d_hl >= nrows) ? 0 : d_u;  // past the end: any valid unit (result unused)
+        }
+      }
+    }
+  };
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's act rows are stored
+  load_down_batch(0);             // stays in flight across the barrier
   trace_mark(p, 8);
-
-  grid_sync(p, 1);
+  lds_barrier();
+  bar_arrive(p);
+  bar_wait(p, 2 * epoch + 2);
   trace_mark(p, 9);
 
   // ---------------- phase D: down projection ----------------
@@ -489,57 +546,55 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
   float* asx = reinterpret_cast<float*>(as + static_cast<size_t>(Ptot) * S_I * 16);
   float* ybuf = asx + static_cast<size_t>(Ptot) * S_I;                         // [wg rows][Ptot]
   float* accD = ybuf + static_cast<size_t>(kFWaves) * rows_per_wave * Ptot;   // [waves][B][64]
-  stage_act_lds<QMODE>(p.act, p.act_stride, Ptot, S_I, as, asx);
-  __syncthreads();
+  stage_rows_lds<QMODE, true>(p.act, p.act_stride, Ptot, S_I, as, asx);
+  lds_barrier();
   trace_mark(p, 10);
   float* ad = accD + static_cast<size_t>(wave) * B * kWave + lane;
   for (int base = 0; base < n_itemsD; base += kChunkD) {
-    if (base > 0) {
-      ZMOE_LOAD_DOWN(base)
-    }
+    if (base > 0) load_down_batch(base);
 #pragma unroll
     for (int j = 0; j < kChunkD; ++j) {
-      const int it = base + j;
-      if (it < n_itemsD) {
-        const int gi = it / TD, t = it - gi * TD;
-        const int slot_raw = gi * RPID + rsD;
-        const int slot = min(slot_raw, slots - 1);
-        const int hl = slot / Uall, u = slot - hl * Uall;
+      if (base + j < n_itemsD) {
+        const int u = ju[j], t = jt[j], hl = jhl[j];
         const int s = t * LI + liD;
         const int nt = L.ucount[u];
+        float sdj, cdj;
+        seg_param_decode<QMODE>(rd[j], sdj, cdj);
         for (int tk = 0; tk < nt; ++tk) {
           const int q = L.upairs[u][tk];
           const float xsum = (QMODE == ZMOE_Q_AFFINE) ? asx[q * S_I + s] : 0.0f;
           const float prev = t == 0 ? 0.0f : ad[tk * kWave];
-          ad[tk * kWave] = seg_accum<QMODE>(prev, sd[j], cd[j], seg_dot_lds<QMODE>(wd[j], as, S_I, q, s), xsum);
+          ad[tk * kWave] = seg_accum<QMODE>(prev, sdj, cdj, seg_dot_lds<QMODE>(wd[j], as, S_I, q, s), xsum);
         }
         if (t == TD - 1) {
           for (int tk = 0; tk < nt; ++tk) {
             const float y = lanes_sum(ad[tk * kWave], LI);
-            if (liD == 0 && slot_raw < slots) ybuf[(wave * rows_per_wave + hl) * Ptot + L.upairs[u][tk]] = round_bf16(y);
+            if (liD == 0 && jvalid[j]) ybuf[(wave * rows_per_wave + hl) * Ptot + L.upairs[u][tk]] = round_bf16(y);
           }
         }
       }
     }
   }
-#undef ZMOE_LOAD_DOWN
-  __syncthreads();
+  lds_barrier();
   trace_mark(p, 11);
 
   // ---------------- combine (+ shared expert) ----------------
   const int wg_row0 = blockIdx.x * kFWaves * rows_per_wave;
-  for (int i = threadIdx.x; i < kFWaves * rows_per_wave * B; i += blockDim.x) {
-    const int r = i / B, b = i - r * B;
-    const int h = wg_row0 + r;
-    if (h >= p.H) continue;
-    const float* yr = ybuf + r * Ptot + b * p.K;
+  const int wg_rows = kFWaves * rows_per_wave;
+  for (int b = 0; b < B; ++b) {
     const float* wk = L.route[b].w;
-    float o = round_bf16(combine_one(p.combine_mode, p.K, [&](int k) { return yr[k]; }, [&](int k) { return wk[k]; }));
-    if (has_shared) o = add_nofma(o, ybuf[r * Ptot + P0 + b]);
-    p.out[static_cast<int64_t>(b) * p.H + h] = static_cast<uint16_t>(f32_to_bf16_bits(o));
+    for (int r = threadIdx.x; r < wg_rows; r += blockDim.x) {
+      const int h = wg_row0 + r;
+      if (h >= p.H) continue;
+      const float* yr = ybuf + r * Ptot + b * K;
+      float o = round_bf16(combine_one(p.combine_mode, K, [&](int k) { return yr[k]; }, [&](int k) { return wk[k]; }));
+      if (has_shared) o = add_nofma(o, ybuf[r * Ptot + P0 + b]);
+      gstore(p.out + static_cast<int64_t>(b) * p.H + h, static_cast<uint16_t>(f32_to_bf16_bits(o)));
+    }
   }
   trace_mark(p, 12);
-  if (p.trace && threadIdx.x == 0) p.trace[blockIdx.x * kTraceSlots + 14] = clock64();
+  if (threadIdx.x == 0) dev_store(p.sync + kEpochWord + blockIdx.x, epoch + 1);
+  if (p.trace && threadIdx.x == 0) gstore(p.trace + blockIdx.x * kTraceSlots + 14, static_cast<unsigned long long>(clock64()));
 }
 
 // ---------------------------------------------------------------------------
@@ -565,7 +620,7 @@ size_t fused_lds_bytes(const zmoe_layer_desc* d, int B) {
   const int Ptot = B * d->top_k + (d->shared_inter > 0 ? B : 0);
   const int G = num_cus();
   const int rows_per_wave = (d->hidden + G * kFWaves - 1) / (G * kFWaves);
-  const size_t front = static_cast<size_t>(B) * S_H * 68 + static_cast<size_t>(B) * d->n_experts * 8 +
+  const size_t front = static_cast<size_t>(B) * S_H * 68 + static_cast<size_t>(B) * d->n_experts * 4 +
                        static_cast<size_t>(kFWaves) * 2 * B * kWave * 4;
   const size_t back = static_cast<size_t>(Ptot) * S_I * 68 + static_cast<size_t>(kFWaves) * rows_per_wave * Ptot * 4 +
                       static_cast<size_t>(kFWaves) * B * kWave * 4;
@@ -574,23 +629,24 @@ size_t fused_lds_bytes(const zmoe_layer_desc* d, int B) {
 
 bool fused_supported(const zmoe_layer_desc* d, int B) {
   if (B < 1 || B > kFMaxB) return false;
-  if (d->hidden % 512 != 0) return false;
+  if (num_cus() > kMaxGrid) return false;
+  if (d->hidden % 512 != 0 || d->hidden / 512 > kMaxNC) return false;
+  if (B * d->top_k > kFThreads) return false;
   if (d->shared_inter > 0 && d->shared_inter != d->inter) return false;
   if (d->n_experts > 1024 || d->top_k > kMaxTopK) return false;
   if (fused_lds_bytes(d, B) > 160 * 1024) return false;
   return true;
 }
 
-// workspace: [0,256) barrier words | flags 2 x G x 128 B | rpart | act | trace
-static size_t off_flags() { return 256; }
-static size_t off_rpart() { return align256(off_flags() + 2ull * num_cus() * kFlagStride * 4); }
+// workspace: barrier-state block | rpart | act | trace
+static size_t off_rpart() { return kSyncBlockBytes; }
 static size_t off_act(const zmoe_layer_desc* d, int B) {
   return align256(off_rpart() + static_cast<size_t>(B) * d->n_experts * (d->hidden / 512) * 4);
 }
 static size_t off_trace(const zmoe_layer_desc* d, int B) {
   const int stride = d->inter > d->shared_inter ? d->inter : d->shared_inter;
   const size_t Ptot = static_cast<size_t>(B) * d->top_k + (d->shared_inter > 0 ? B : 0);
-  return align256(off_act(d, B) + Ptot * stride * 4);
+  return align256(off_act(d, B) + Ptot * stride * 2);
 }
 
 size_t fused_workspace_bytes(const zmoe_layer_desc* d, int B) {
@@ -603,22 +659,31 @@ size_t fused_trace_info(const zmoe_layer_desc* d, int B, int* n_blocks, int* n_s
   return off_trace(d, B);
 }
 
-template <int QMODE>
+template <int QMODE, int P>
 static int launch_fused_t(hipStream_t st, const FusedParams& fp, size_t lds) {
   static bool prepared = false;
   int occ = 0;
+  const void* fn = reinterpret_cast<const void*>(&k_moe_decode<QMODE, P>);
   if (!prepared) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_moe_decode<QMODE>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     prepared = true;
   }
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(&k_moe_decode<QMODE>),
-                                                   kFThreads, lds) != hipSuccess ||
-      occ < 1) {
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, kFThreads, lds) != hipSuccess || occ < 1) {
     return fail(ZMOE_EUNSUPPORTED, "[moe_layer] single-launch kernel cannot be resident on every CU");
   }
-  hipLaunchKernelGGL((k_moe_decode<QMODE>), dim3(num_cus()), dim3(kFThreads), lds, st, fp);
+  hipLaunchKernelGGL((k_moe_decode<QMODE, P>), dim3(num_cus()), dim3(kFThreads), lds, st, fp);
   return check_launch("moe_layer(single launch)");
+}
+
+template <int QMODE>
+static int launch_fused_q(hipStream_t st, const FusedParams& fp, size_t lds) {
+  switch (route_slots(fp.E)) {
+    case 1: return launch_fused_t<QMODE, 1>(st, fp, lds);
+    case 2: return launch_fused_t<QMODE, 2>(st, fp, lds);
+    case 4: return launch_fused_t<QMODE, 4>(st, fp, lds);
+    case 8: return launch_fused_t<QMODE, 8>(st, fp, lds);
+    default: return launch_fused_t<QMODE, 16>(st, fp, lds);
+  }
 }
 
 int launch_fused(hipStream_t st, const zmoe_layer_desc* d, const void* x, int B, void* out, uint32_t* out_idx,
@@ -658,17 +723,16 @@ int launch_fused(hipStream_t st, const zmoe_layer_desc* d, const void* x, int B,
     fp.b[i] = bs[i];
   }
   char* base = static_cast<char*>(workspace);
-  fp.bar = reinterpret_cast<unsigned*>(base);
-  fp.flags = reinterpret_cast<unsigned*>(base + off_flags());
+  fp.sync = reinterpret_cast<unsigned*>(base);
   fp.rpart = reinterpret_cast<float*>(base + off_rpart());
-  fp.act = reinterpret_cast<float*>(base + off_act(d, B));
+  fp.act = reinterpret_cast<uint16_t*>(base + off_act(d, B));
   fp.act_stride = d->inter > d->shared_inter ? d->inter : d->shared_inter;
   fp.out_idx = out_idx;
   fp.out_w = out_w;
   fp.trace = (d->flags & ZMOE_LAYER_TRACE) ? reinterpret_cast<unsigned long long*>(base + off_trace(d, B)) : nullptr;
   const size_t lds = fused_lds_bytes(d, B);
-  if (d->quant_mode == ZMOE_Q_AFFINE) return launch_fused_t<ZMOE_Q_AFFINE>(st, fp, lds);
-  return launch_fused_t<ZMOE_Q_MXFP4>(st, fp, lds);
+  if (d->quant_mode == ZMOE_Q_AFFINE) return launch_fused_q<ZMOE_Q_AFFINE>(st, fp, lds);
+  return launch_fused_q<ZMOE_Q_MXFP4>(st, fp, lds);
 }
 
 }  // namespace zmoe

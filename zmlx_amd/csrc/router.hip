@@ -85,8 +85,7 @@ __global__ __launch_bounds__(256) void k_dense_logits(const uint16_t* __restrict
 // code the single-launch layer kernel runs.
 // ---------------------------------------------------------------------------
 struct RouterBlockLds {
-  float v[4][kRouterMaxE];
-  float aff[4][kRouterMaxE];
+  float grow[4][kRouterMaxE];
   RouteLds r[4];
 };
 
@@ -98,14 +97,14 @@ __global__ __launch_bounds__(256) void k_route_rows(const void* __restrict__ log
   const int row = blockIdx.x * 4 + wave;
   if (row >= B) return;  // wave-private LDS only: no block barriers
   const int lane = __lane_id();
-  float* v = S.v[wave];
-  for (int e = lane; e < a.E; e += kWave) {
-    const int64_t i = static_cast<int64_t>(row) * a.E + e;
-    v[e] = (dtype == ZMOE_DT_F32) ? static_cast<const float*>(logits)[i]
-                                  : bf16_bits_to_f32(static_cast<const uint16_t*>(logits)[i]);
-  }
-  wave_lds_sync();
-  route_row(a, v, S.aff[wave], S.r[wave]);
+  const int64_t base = static_cast<int64_t>(row) * a.E;
+  route_row_any(
+      a,
+      [&](int e) {
+        return (dtype == ZMOE_DT_F32) ? static_cast<const float*>(logits)[base + e]
+                                      : bf16_bits_to_f32(static_cast<const uint16_t*>(logits)[base + e]);
+      },
+      *(ZMOE_LDS RouteLds*)(&S.r[wave]), (ZMOE_LDS float*)(S.grow[wave]));
   if (lane < a.k) {
     const int64_t o = static_cast<int64_t>(row) * a.k + lane;
     const float w = S.r[wave].w[lane];

@@ -18,6 +18,56 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
 
+// Address-space qualifiers: pointers that reach a kernel through a struct or
+// an array lose their address space and compile to flat accesses, which
+// also count against the LDS wait counter (every LDS wait then waits for
+// in-flight HBM loads).  Accesses on hot paths go through these instead.
+#define ZMOE_GLOBAL __attribute__((address_space(1)))
+#define ZMOE_LDS __attribute__((address_space(3)))
+
+// (The host compilation pass never runs these; it only parses them.)
+template <typename T>
+__device__ __forceinline__ T gload(const T* p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  T v;
+  __builtin_memcpy(&v, (const ZMOE_GLOBAL T*)(p), sizeof(T));
+  return v;
+#else
+  return *p;
+#endif
+}
+
+template <typename T>
+__device__ __forceinline__ void gstore(T* p, T v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_memcpy((ZMOE_GLOBAL T*)(p), &v, sizeof(T));
+#else
+  *p = v;
+#endif
+}
+
+// Device-scope (all XCDs) coherent accesses for data exchanged between
+// workgroups inside one launch.
+// Workgroup barrier that orders LDS only: unlike __syncthreads() it does
+// not wait for this wave's outstanding global loads (prefetches stay in
+// flight across it).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <typename T>
+__device__ __forceinline__ T dev_load(const T* p) {
+  return __hip_atomic_load((ZMOE_GLOBAL T*)(const_cast<T*>(p)), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename T>
+__device__ __forceinline__ void dev_store(T* p, T v) {
+  __hip_atomic_store((ZMOE_GLOBAL T*)(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---------------------------------------------------------------------------
 // bf16 <-> fp32
 // ---------------------------------------------------------------------------
@@ -57,19 +107,59 @@ __device__ __forceinline__ uint32_t swiglu_bf16(float g_bf16, float u_bf16) {
 // ---------------------------------------------------------------------------
 // Wave reductions
 // ---------------------------------------------------------------------------
+// Sums over aligned groups of WIDTH lanes with DPP row operations (no LDS
+// traffic): pair, quad, half-row (8) and row (16) steps; 32- and 64-lane
+// groups add the rows through lane reads.  Every lane of a group receives
+// the same value, and every kernel uses these same helpers, so results are
+// reproducible across kernels.
+#define ZMOE_DPP_ADD(v, ctrl)                                                                         \
+  (v) = (v) + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), \
+                                                                    (ctrl), 0xF, 0xF, false))
+#define ZMOE_DPP_MAX(v, ctrl)                                                                               \
+  (v) = fmaxf((v), __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), \
+                                                                         (ctrl), 0xF, 0xF, false)))
+
+constexpr int kDppQuadSwap1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kDppQuadSwap2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+__device__ __forceinline__ float readlane_f(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
 template <int WIDTH>
 __device__ __forceinline__ float wave_sum_width(float v) {
-#pragma unroll
-  for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WIDTH);
+  static_assert(WIDTH == 2 || WIDTH == 4 || WIDTH == 8 || WIDTH == 16 || WIDTH == 32 || WIDTH == 64, "width");
+  ZMOE_DPP_ADD(v, kDppQuadSwap1);
+  if (WIDTH >= 4) ZMOE_DPP_ADD(v, kDppQuadSwap2);
+  if (WIDTH >= 8) ZMOE_DPP_ADD(v, kDppHalfMirror);
+  if (WIDTH >= 16) ZMOE_DPP_ADD(v, kDppRowMirror);
+  if (WIDTH == 32) v += __shfl_xor(v, 16);
+  if (WIDTH == 64) v = (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
   return v;
 }
 
 __device__ __forceinline__ float wave_sum(float v) { return wave_sum_width<kWave>(v); }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
+  ZMOE_DPP_MAX(v, kDppQuadSwap1);
+  ZMOE_DPP_MAX(v, kDppQuadSwap2);
+  ZMOE_DPP_MAX(v, kDppHalfMirror);
+  ZMOE_DPP_MAX(v, kDppRowMirror);
+  return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+
+// Runtime group width L in {8, 16, 32, 64} (lanes sharing one weight row).
+__device__ __forceinline__ float lanes_sum(float v, int L) {
+  switch (L) {
+    case 64: return wave_sum_width<64>(v);
+    case 32: return wave_sum_width<32>(v);
+    case 16: return wave_sum_width<16>(v);
+    case 8: return wave_sum_width<8>(v);
+    case 4: return wave_sum_width<4>(v);
+    default: return wave_sum_width<2>(v);
+  }
 }
 
 // ---------------------------------------------------------------------------

@@ -11,6 +11,11 @@
 
 namespace zmoe {
 
+// Leading bytes of the layer workspace reserved for the single-launch
+// kernel's barrier state; the multi-kernel path's buffers start after it.
+constexpr size_t kSyncBlockBytes = 16384;
+constexpr size_t kSyncErrorByte = 128;
+
 void set_error(const std::string& msg);
 
 inline int fail(int code, const std::string& msg) {

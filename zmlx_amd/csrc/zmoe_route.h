@@ -1,12 +1,12 @@
-// Wave-level routing over one token row held in LDS, shared by the
-// standalone router kernels and the single-launch layer kernel so both
-// produce bit-identical routing.  Written for small code size (loops, no
-// dynamically indexed register arrays): the whole wave cooperates on one
-// row; values live in wave-private LDS.
+// Wave-level routing of one token row, shared by the standalone router
+// kernels and the single-launch layer kernel so both produce bit-identical
+// routing.
 //
-// Selection order everywhere: value descending, lower expert index first on
-// ties.  Top-k is a radix select of the k-th key on wave ballots, then the
-// k winners are ranked.
+// Layout: lane l holds experts l, l+64, ... (P values per lane, P = 1..16
+// for E <= 64P) in registers; wave-private LDS holds only the short winner
+// list.  Top-k is a radix select of the k-th key on wave ballots (32 steps,
+// no memory traffic), then the winners are ranked.  Selection order
+// everywhere: value descending, lower expert index first on ties.
 #pragma once
 
 #include "zmoe_common.h"
@@ -15,16 +15,18 @@ namespace zmoe {
 
 constexpr int kMaxTopK = 16;
 
-// Per-wave LDS scratch of the router (besides the two E-float rows `v`,
-// the working values, and `aff`, the sigmoid affinities of the grouped
-// router, which the caller places).
+// Per-wave LDS scratch of the router.
 struct RouteLds {
-  float gsc[64];    // group scores
-  int cnt;          // winner list length
+  float gsc[64];  // group scores (grouped router)
+  int cnt;        // winner list length
   uint32_t wkey[kMaxTopK];
   int widx[kMaxTopK];
-  int sel[kMaxTopK];
-  float w[kMaxTopK];
+  float wval[kMaxTopK];
+  float waux[kMaxTopK];
+  int sel[kMaxTopK];   // result: selected experts in order
+  float sval[kMaxTopK];
+  float saux[kMaxTopK];
+  float w[kMaxTopK];   // result: weights
 };
 
 // Orders LDS traffic between the lanes of one wave (compiler barrier; the
@@ -44,52 +46,60 @@ __device__ __forceinline__ uint64_t lanes_below_mask(int lane) {
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
 
-// Sum / max of v[0..n) over the wave: each lane folds its entries
-// (lane, lane+64, ...) in order, then a fixed butterfly -- reproducible.
-__device__ __forceinline__ float lds_row_sum(const float* v, int n) {
+// Wave sum / max of a lane-strided row: each lane folds its P values in
+// slot order, then a fixed butterfly -- reproducible.
+template <int P>
+__device__ __forceinline__ float reg_row_sum(const float (&v)[P], int E) {
   float s = 0.0f;
-  for (int e = __lane_id(); e < n; e += kWave) s += v[e];
+#pragma unroll
+  for (int i = 0; i < P; ++i)
+    if (__lane_id() + 64 * i < E) s += v[i];
   return wave_sum(s);
 }
 
-__device__ __forceinline__ float lds_row_max(const float* v, int n) {
+template <int P>
+__device__ __forceinline__ float reg_row_max(const float (&v)[P], int E) {
   float m = -INFINITY;
-  for (int e = __lane_id(); e < n; e += kWave) m = fmaxf(m, v[e]);
+#pragma unroll
+  for (int i = 0; i < P; ++i)
+    if (__lane_id() + 64 * i < E) m = fmaxf(m, v[i]);
   return wave_max(m);
 }
 
-// Writes into R.sel[0..k) the k largest of vals[0..n) ordered by
-// (value desc, index asc).  All 64 lanes must call it.
-__device__ __forceinline__ void lds_topk(const float* vals, int n, int k, RouteLds& R) {
+// k largest of v[0..n) (lane-strided registers), ties to the lower index.
+// Fills R.sel / R.sval (value) / R.saux (aux[] of the winner) in order
+// (value desc, index asc).  All 64 lanes call it.
+template <int P>
+__device__ __forceinline__ void reg_topk(const float (&v)[P], const float (&aux)[P], int n, int k, ZMOE_LDS RouteLds& R) {
   const int lane = __lane_id();
-  uint32_t T = 0;
+  uint32_t key[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) key[i] = (lane + 64 * i < n) ? order_key(v[i]) : 0u;
+  uint32_t T = 0;  // largest threshold with |{key >= T}| >= k
   for (int bit = 31; bit >= 0; --bit) {
     const uint32_t cand = T | (1u << bit);
     int cnt = 0;
-    for (int e0 = 0; e0 < n; e0 += kWave) {
-      const int e = e0 + lane;
-      cnt += __popcll(__ballot(e < n && order_key(vals[e]) >= cand));
-    }
+#pragma unroll
+    for (int i = 0; i < P; ++i) cnt += __popcll(__ballot(key[i] >= cand));
     if (cnt >= k) T = cand;
   }
   int need = k;
-  for (int e0 = 0; e0 < n; e0 += kWave) {
-    const int e = e0 + lane;
-    need -= __popcll(__ballot(e < n && order_key(vals[e]) > T));
-  }
+#pragma unroll
+  for (int i = 0; i < P; ++i) need -= __popcll(__ballot(key[i] > T));
   if (lane == 0) R.cnt = 0;
   wave_lds_sync();
-  for (int e0 = 0; e0 < n; e0 += kWave) {
-    const int e = e0 + lane;
-    const uint32_t key = e < n ? order_key(vals[e]) : 0u;
-    const bool tie = e < n && key == T;
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const bool tie = key[i] == T && key[i] != 0u;
     const uint64_t tm = __ballot(tie);
-    const bool take = (e < n && key > T) || (tie && __popcll(tm & lanes_below_mask(lane)) < need);
+    const bool take = key[i] > T || (tie && __popcll(tm & lanes_below_mask(lane)) < need);
     need -= min(need, __popcll(tm));
     if (take) {
-      const int pos = atomicAdd(&R.cnt, 1);
-      R.wkey[pos] = key;
-      R.widx[pos] = e;
+      const int pos = __hip_atomic_fetch_add(&R.cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+      R.wkey[pos] = key[i];
+      R.widx[pos] = lane + 64 * i;
+      R.wval[pos] = v[i];
+      R.waux[pos] = aux[i];
     }
   }
   wave_lds_sync();
@@ -103,6 +113,8 @@ __device__ __forceinline__ void lds_topk(const float* vals, int n, int k, RouteL
       rank += (kj > kr || (kj == kr && ej < er)) ? 1 : 0;
     }
     R.sel[rank] = er;
+    R.sval[rank] = R.wval[lane];
+    R.saux[rank] = R.waux[lane];
   }
   wave_lds_sync();
 }
@@ -134,65 +146,83 @@ struct RouteArgs {
   int w_bf16;         // round the weights to bf16 (topk-logits router in a bf16 model)
 };
 
-// Routes the row already written to v[0..E) (entries are logits); `aff` is
-// E floats of scratch (grouped router only).  Results: R.sel[0..k),
-// R.w[0..k).  All 64 lanes must call it.
-__device__ __noinline__ void route_row(const RouteArgs& a, float* v, float* aff, RouteLds& R) {
+// One row of scores in lane-strided registers (passed by value so a call
+// keeps it in VGPRs).
+template <int P>
+struct RowVals {
+  float v[P];
+};
+
+// Routes one row of logits given lane-strided in row.v (entries >= E
+// ignored).  Results: R.sel[0..k), R.w[0..k).  All 64 lanes call it.
+// `grow` is E floats of wave-private LDS (grouped router only).
+template <int P>
+__device__ __forceinline__ void route_row(const RouteArgs a, RowVals<P> row, ZMOE_LDS RouteLds& R, ZMOE_LDS float* grow) {
+  float (&v)[P] = row.v;
   const int lane = __lane_id();
   const int E = a.E, k = a.k;
+  float aux[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) aux[i] = 0.0f;
   if (a.kind == kRouteSoftmaxProbs) {
     // Qwen (moe_mlp.py:255-266): precise softmax -> bf16 probs -> top-k ->
     // /bf16(sum) in bf16 when norm
-    const float m = lds_row_max(v, E);
-    for (int e = lane; e < E; e += kWave) v[e] = expf(v[e] - m);
-    wave_lds_sync();
-    const float s = lds_row_sum(v, E);
-    for (int e = lane; e < E; e += kWave) v[e] = div_to_bf16(v[e], s);
-    wave_lds_sync();
-    lds_topk(v, E, k, R);
+    const float m = reg_row_max(v, E);
+#pragma unroll
+    for (int i = 0; i < P; ++i) v[i] = expf(v[i] - m);
+    const float s = reg_row_sum(v, E);
+#pragma unroll
+    for (int i = 0; i < P; ++i) v[i] = div_to_bf16(v[i], s);
+    reg_topk(v, aux, E, k, R);
     float tot = 0.0f;
-    for (int r = 0; r < k; ++r) tot += v[R.sel[r]];
+    for (int r = 0; r < k; ++r) tot += R.sval[r];
     const float sb = round_bf16(tot);
-    if (lane < k) {
-      const float pr = v[R.sel[lane]];
-      R.w[lane] = a.norm ? div_to_bf16(pr, sb) : pr;
-    }
+    if (lane < k) R.w[lane] = a.norm ? div_to_bf16(R.sval[lane], sb) : R.sval[lane];
   } else if (a.kind == kRouteTopkLogits) {
     // moe.topk_gating_softmax (moe.py:1239-1396), f32 compute
     if (a.bias == nullptr && a.norm) {
-      lds_topk(v, E, k, R);
-      const float m = v[R.sel[0]];
+      reg_topk(v, aux, E, k, R);
+      const float m = R.sval[0];
       float s = 0.0f;
-      for (int r = 0; r < k; ++r) s += expf(v[R.sel[r]] - m);
-      if (lane < k) R.w[lane] = expf(v[R.sel[lane]] - m) / s;
+      for (int r = 0; r < k; ++r) s += expf(R.sval[r] - m);
+      if (lane < k) R.w[lane] = expf(R.sval[lane] - m) / s;
     } else {
-      const float m = lds_row_max(v, E);
-      for (int e = lane; e < E; e += kWave) v[e] = expf(v[e] - m);
-      wave_lds_sync();
-      const float s = lds_row_sum(v, E);
-      for (int e = lane; e < E; e += kWave) v[e] = v[e] / s + (a.bias ? a.bias[e] : 0.0f);
-      wave_lds_sync();
-      lds_topk(v, E, k, R);
+      const float m = reg_row_max(v, E);
+#pragma unroll
+      for (int i = 0; i < P; ++i) v[i] = expf(v[i] - m);
+      const float s = reg_row_sum(v, E);
+#pragma unroll
+      for (int i = 0; i < P; ++i) {
+        const int e = lane + 64 * i;
+        v[i] = v[i] / s + ((a.bias && e < E) ? gload(a.bias + e) : 0.0f);
+      }
+      reg_topk(v, aux, E, k, R);
       float t = 0.0f;
-      for (int r = 0; r < k; ++r) t += v[R.sel[r]];
-      if (lane < k) R.w[lane] = a.norm ? v[R.sel[lane]] / (t + 1e-20f) : v[R.sel[lane]];
+      for (int r = 0; r < k; ++r) t += R.sval[r];
+      if (lane < k) R.w[lane] = a.norm ? R.sval[lane] / (t + 1e-20f) : R.sval[lane];
     }
     if (a.w_bf16 && lane < k) R.w[lane] = round_bf16(R.w[lane]);
   } else {
     // DeepSeek/GLM grouped sigmoid router (moe.py:1501-1742,
-    // deepseek_router.py:118)
-    for (int e = lane; e < E; e += kWave) {
-      const float af = sigmoid_abs(v[e]);
-      aff[e] = af;
-      v[e] = af + a.bias[e];
+    // deepseek_router.py:118): scores = sigmoid + bias select, weights are
+    // the normalised sigmoids
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      const int e = lane + 64 * i;
+      aux[i] = sigmoid_abs(v[i]);
+      v[i] = aux[i] + (e < E ? gload(a.bias + e) : 0.0f);
     }
-    wave_lds_sync();
     if (a.n_group > 1 && a.topk_group < a.n_group) {
-      const int gsz = E / a.n_group;
-      if (lane < a.n_group) {
+      const int gsz = E / a.n_group, ng = a.n_group, kg = a.topk_group;
+#pragma unroll
+      for (int i = 0; i < P; ++i)
+        if (lane + 64 * i < E) grow[lane + 64 * i] = v[i];
+      wave_lds_sync();
+      if (lane < ng) {
         float t1 = -INFINITY, t2 = -INFINITY;
+#pragma unroll 8
         for (int j = 0; j < gsz; ++j) {
-          const float x = v[lane * gsz + j];
+          const float x = grow[lane * gsz + j];
           if (x > t1) {
             t2 = t1;
             t1 = x;
@@ -203,33 +233,73 @@ __device__ __noinline__ void route_row(const RouteArgs& a, float* v, float* aff,
         R.gsc[lane] = t1 + t2;
       }
       wave_lds_sync();
-      // keep the topk_group best groups (ties -> lower group index): mark
-      // them through the same radix select
+      // keep the topk_group best groups (ties -> lower group index)
+      const uint32_t gk = lane < ng ? order_key(R.gsc[lane]) : 0u;
       uint32_t T = 0;
-      const int ng = a.n_group, kg = a.topk_group;
       for (int bit = 31; bit >= 0; --bit) {
         const uint32_t cand = T | (1u << bit);
-        if (__popcll(__ballot(lane < ng && order_key(R.gsc[lane]) >= cand)) >= kg) T = cand;
+        if (__popcll(__ballot(gk >= cand)) >= kg) T = cand;
       }
-      int need = kg - __popcll(__ballot(lane < ng && order_key(R.gsc[lane]) > T));
-      const uint32_t gk = lane < ng ? order_key(R.gsc[lane]) : 0u;
-      const uint64_t tm = __ballot(lane < ng && gk == T);
-      const bool keep = lane < ng && (gk > T || (gk == T && __popcll(tm & lanes_below_mask(lane)) < need));
+      const int need = kg - __popcll(__ballot(gk > T));
+      const uint64_t tm = __ballot(gk == T && gk != 0u);
+      const bool keep = gk > T || (gk == T && gk != 0u && __popcll(tm & lanes_below_mask(lane)) < need);
       const uint64_t keepm = __ballot(keep);
-      for (int e = lane; e < E; e += kWave)
-        if (!((keepm >> (e / gsz)) & 1ull)) v[e] = 0.0f;
-      wave_lds_sync();
+#pragma unroll
+      for (int i = 0; i < P; ++i) {
+        const int e = lane + 64 * i;
+        if (e < E && !((keepm >> (e / gsz)) & 1ull)) v[i] = 0.0f;
+      }
     }
-    lds_topk(v, E, k, R);
+    reg_topk(v, aux, E, k, R);
     float s = 0.0f;
-    for (int r = 0; r < k; ++r) s += aff[R.sel[r]];
+    for (int r = 0; r < k; ++r) s += R.saux[r];
     if (lane < k) {
-      float x = aff[R.sel[lane]] / s;
+      float x = R.saux[lane] / s;
       if (a.scale != 1.0f) x = x * a.scale;
       R.w[lane] = x;
     }
   }
   wave_lds_sync();
+}
+
+// Values per lane needed for E experts.
+__host__ __device__ constexpr int route_slots(int E) { return E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16; }
+
+// Loads a row through `get(e)` into P lane-strided registers and routes it.
+template <int P, typename F>
+__device__ __forceinline__ void route_row_p(const RouteArgs& a, F get, ZMOE_LDS RouteLds& R, ZMOE_LDS float* grow) {
+  const int lane = __lane_id();
+  RowVals<P> row;
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const int e = lane + 64 * i;
+    row.v[i] = e < a.E ? get(e) : -INFINITY;
+  }
+  route_row<P>(a, row, R, grow);
+}
+
+// Loads a row through `get(e)` into lane-strided registers and routes it with
+// the smallest register footprint that holds E.
+template <typename F>
+__device__ __forceinline__ void route_row_any(const RouteArgs& a, F get, ZMOE_LDS RouteLds& R, ZMOE_LDS float* grow) {
+  const int lane = __lane_id();
+#define ZMOE_ROUTE_P(PP)                                             \
+  {                                                                  \
+    RowVals<PP> row;                                                 \
+    _Pragma("unroll") for (int i = 0; i < PP; ++i) {                 \
+      const int e = lane + 64 * i;                                   \
+      row.v[i] = e < a.E ? get(e) : -INFINITY;                       \
+    }                                                                \
+    route_row<PP>(a, row, R, grow);                                  \
+  }
+  switch (route_slots(a.E)) {
+    case 1: ZMOE_ROUTE_P(1) break;
+    case 2: ZMOE_ROUTE_P(2) break;
+    case 4: ZMOE_ROUTE_P(4) break;
+    case 8: ZMOE_ROUTE_P(8) break;
+    default: ZMOE_ROUTE_P(16) break;
+  }
+#undef ZMOE_ROUTE_P
 }
 
 }  // namespace zmoe

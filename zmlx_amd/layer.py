@@ -151,9 +151,9 @@ class QuantizedMoELayer:
     def _workspace(self, B: int) -> torch.Tensor:
         ws = self._ws.get(B)
         if ws is None:
-            # zero-filled once: the first 256 bytes are the fused kernel's
-            # barrier counters, which every call leaves at zero again
-            ws = torch.zeros(max(self.workspace_bytes(B), 256), dtype=torch.uint8, device=self.device)
+            # zero-filled once: the leading block holds the fused kernel's
+            # barrier state (counters that only increase from call to call)
+            ws = torch.zeros(self.workspace_bytes(B), dtype=torch.uint8, device=self.device)
             self._ws[B] = ws
         return ws
 
