@@ -9,29 +9,40 @@ cannot hold the working set.  Decode batch B (default 1) of bf16 N(0,1)
 tokens; synthetic, seeded data.
 
 A step = one pass of the MoE block over the batch through all 48 layer copies
-(48 layer calls).  Reported:
+(48 layer calls, replayed from one HIP graph).  Reported:
   value       us per token per layer call at B (lower is better)
   gbps        algorithmic HBM bytes per layer call / layer time
-  roofline    of the dominant kernel, timed with HIP events on its stream
+  roofline    of the dominant kernel -- the single-launch layer kernel
+              k_moe_decode, one launch per layer call -- from HIP events on
+              the stream it runs on, around the timed region; `traffic` is the
+              measured HBM bytes per launch from the committed rocprofv3
+              counter summary (profiles/k_moe_decode_qwen3_b1_traffic.json)
   cpu_baseline  this repo's C++/OpenMP restatement of the unpatched MLX path
               (MLX is not installable offline) on the host cores, rank 0.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B]
+       python bench.py --profile-run          # short run for rocprofv3 --pmc
+       python bench.py --summarize-pmc DIR     # FETCH_SIZE/WRITE_SIZE -> traffic
 """
 
 from __future__ import annotations
 
 import argparse
+import csv
 import json
 import os
 import sys
 import time
+from pathlib import Path
 
 METRIC = "MoE-layer decode µs/token + HBM GB/s (% roofline), Qwen3-30B-A3B shape 4-bit"
 HBM_PEAK_GBPS = 8000.0
 
 H, E, K, I, GS = 2048, 128, 8, 768, 64
 LAYERS = 48
+ROOT = Path(__file__).resolve().parent
+TRAFFIC_FILE = ROOT / "profiles" / "k_moe_decode_qwen3_b1_traffic.json"
+COPY_BYTES = 256 << 20  # calibration copy of --profile-run: reads and writes this many bytes
 
 
 def log(msg: str) -> None:
@@ -95,8 +106,11 @@ def capture_step(layers, x):
     return graph
 
 
-def time_layers(layers, x, steps: int, warmup: int, use_graph: bool = True) -> float:
-    """Average ms per step (one call of every layer copy)."""
+def time_layers(layers, x, steps: int, warmup: int, use_graph: bool = True, per_step: list | None = None) -> float:
+    """Average ms per step (one call of every layer copy), from HIP events
+    recorded on the stream the layer kernels run on (torch's current stream,
+    where the graph is replayed).  If ``per_step`` is a list, the ms of each
+    step is appended to it (events between steps)."""
     import torch
 
     if use_graph:
@@ -109,14 +123,15 @@ def time_layers(layers, x, steps: int, warmup: int, use_graph: bool = True) -> f
     for _ in range(warmup):
         run()
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    evs[0].record()
+    for i in range(steps):
         run()
-    stop.record()
+        evs[i + 1].record()
     torch.cuda.synchronize()
-    return start.elapsed_time(stop) / steps
+    if per_step is not None:
+        per_step.extend(evs[i].elapsed_time(evs[i + 1]) for i in range(steps))
+    return evs[0].elapsed_time(evs[-1]) / steps
 
 
 def unique_experts(layers, x):
@@ -133,28 +148,69 @@ def unique_experts(layers, x):
     return counts, idxs
 
 
-def dominant_kernel(layers, x, idxs, steps: int):
-    """Time the fused gate/up+SwiGLU kernel alone over the rotated copies
-    (HIP events on the torch stream the kernel is launched on)."""
+def load_traffic():
+    """HBM bytes per k_moe_decode launch measured by rocprofv3 (FETCH_SIZE and
+    WRITE_SIZE, calibrated on a copy kernel), if the summary is committed."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return t
+    except (OSError, ValueError):
+        return None
+
+
+def profile_run(args) -> int:
+    """Short run for `rocprofv3 --pmc`: one calibration copy of COPY_BYTES
+    (torch's copy kernel), then graph replays of the B=1 workload."""
     import torch
 
-    import zmlx_amd as Z
-
-    def run():
-        for layer, idx in zip(layers, idxs):
-            gate, up = layer._proj["gate"], layer._proj["up"]
-            Z.gather_qmm_swiglu(x[:, None, None, :], *gate, *up, rhs_indices=idx[:, None, :])
-
-    run()
+    dev = torch.device("cuda:0")
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
-        run()
-    stop.record()
+    dst.copy_(src)
     torch.cuda.synchronize()
-    return start.elapsed_time(stop) * 1e3 / (steps * len(layers))  # us per launch
+    del src, dst
+    layers, _ = build_layers(dev, args.layers)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+    x = torch.randn((args.batch, H), generator=gen, device=dev).to(torch.bfloat16)
+    ms = time_layers(layers, x, args.steps, args.warmup)
+    log(f"profile run: {ms * 1e3 / len(layers):.2f} us per layer call")
+    return 0
+
+
+def summarize_pmc(fetch_dir: str, write_dir: str) -> int:
+    """Turns two rocprofv3 --pmc runs of --profile-run (FETCH_SIZE, then
+    WRITE_SIZE; KiB per dispatch) into bytes per k_moe_decode launch, each
+    scaled by the factor that makes the calibration copy read/write exactly
+    COPY_BYTES."""
+    def per_kernel(d, counter):
+        vals = {}
+        for path in Path(d).rglob("*counter_collection.csv"):
+            with open(path) as f:
+                for row in csv.DictReader(f):
+                    if row.get("Counter_Name") != counter:
+                        continue
+                    vals.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+        return vals
+
+    out = {}
+    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        vals = per_kernel(d, counter)
+        copy = [v for k, vs in vals.items() if "copy" in k.lower() or "elementwise" in k.lower() for v in vs]
+        dec = [v for k, vs in vals.items() if "k_moe_decode" in k for v in vs]
+        if not copy or not dec:
+            print(f"no copy / k_moe_decode dispatches for {counter} in {d}", file=sys.stderr)
+            return 1
+        copy_kib = max(copy)
+        factor = (COPY_BYTES / 1024.0) / copy_kib
+        dec_kib = sum(dec) / len(dec)
+        out[counter] = {"copy_kib": copy_kib, "factor": factor, "k_moe_decode_kib_avg": dec_kib,
+                        "k_moe_decode_bytes": dec_kib * 1024.0 * factor, "dispatches": len(dec)}
+    out["bytes_per_launch"] = out["FETCH_SIZE"]["k_moe_decode_bytes"] + out["WRITE_SIZE"]["k_moe_decode_bytes"]
+    print(json.dumps(out, indent=1))
+    return 0
 
 
 def cpu_baseline(base, layer0, x_host, budget_s: float = 12.0, max_tokens: int = 4096):
@@ -206,7 +262,11 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
+    ap.add_argument("--profile-run", action="store_true", help="short run for rocprofv3 counter passes")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     args = ap.parse_args()
+    if args.summarize_pmc:
+        return summarize_pmc(*args.summarize_pmc)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -218,6 +278,8 @@ def main() -> int:
 
     import zmlx_amd  # noqa: F401  (fails loudly if the HIP library is missing)
 
+    if args.profile_run:
+        return profile_run(args)
     dev = torch.device("cuda:0")
     log(f"building {args.layers} layer copies (this takes a few seconds)")
     layers, base = build_layers(dev, args.layers)
@@ -231,25 +293,29 @@ def main() -> int:
         counts, idxs = unique_experts(layers, x)
         steps = args.steps if B == args.batch else max(5, args.steps // 4)
         log(f"B={B}: timing {steps} steps x {len(layers)} layers")
-        ms = time_layers(layers, x, steps, args.warmup, use_graph=not args.no_graph)
+        step_ms: list = []
+        ms = time_layers(layers, x, steps, args.warmup, use_graph=not args.no_graph, per_step=step_ms)
         layer_us = ms * 1e3 / len(layers)
+        q = sorted(v * 1e3 / len(layers) for v in step_ms)
+        pct = {f"p{p}": round(q[min(len(q) - 1, int(p / 100 * len(q)))], 3) for p in (10, 50, 90)}
         avg_unique = sum(counts) / len(counts)
         alg_bytes = avg_unique * per_expert_bytes() + E * H * 2 + 4 * B * H
         gbps = alg_bytes / (layer_us * 1e-6) / 1e9
         rec = {"us_per_token": round(layer_us / B, 3), "us_per_layer_call": round(layer_us, 3),
                "gbps": round(gbps, 1), "roofline_frac": round(gbps / HBM_PEAK_GBPS, 4),
                "unique_experts": round(avg_unique, 2), "alg_bytes_per_call": int(alg_bytes), "steps": steps,
-               "ms_per_step": round(ms, 4)}
+               "ms_per_step": round(ms, 4), "us_per_layer_call_pct": pct}
         per_b[str(B)] = rec
         if B == args.batch:
             main_rec = rec
-            kus = dominant_kernel(layers, x, idxs, max(5, steps // 2))
-            kbytes = avg_unique * 2 * I * (H // 2 + (H // GS) * 4) + B * H * 2 + B * K * I * 2
-            kgbps = kbytes / (kus * 1e-6) / 1e9
-            roof = {"bound": "hbm", "achieved": round(kgbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                    "frac": round(kgbps / HBM_PEAK_GBPS, 4), "traffic": None,
-                    "kernel": "k_gather_qmv<SWIGLU> (gate/up + SwiGLU)", "avg_launch_us": round(kus, 3),
-                    "alg_bytes_per_launch": int(kbytes)}
+            # one k_moe_decode launch per layer call: the timed region holds
+            # steps x layers launches and nothing else
+            tr = load_traffic() if B == 1 else None
+            roof = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                    "traffic": int(tr["bytes_per_launch"]) if tr else None,
+                    "kernel": "k_moe_decode (single-launch MoE layer)", "avg_launch_us": round(layer_us, 3),
+                    "alg_bytes_per_launch": int(alg_bytes)}
         log(f"B={B}: {rec}")
 
     cpu = None
