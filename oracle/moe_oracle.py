@@ -25,6 +25,14 @@ wherever MLX holds a bf16 array; ``bf16_round`` is the only rounding primitive
 Points where MLX's own choice is not visible from the reference (reduction
 order of a bf16 ``sum``, argpartition tie order) are stated in each docstring
 and only pinned by tolerance / tie-set rules in the tests.
+
+Pinning (tests/test_oracle_pins.py, tests/test_golden.py): every function is
+checked against closed forms, exhaustive format tables, the reference's known
+answers, brute force or an independent C++ restatement.  Parity unpinned
+(nothing without MLX can fix them): ``quantize_affine`` versus MLX's
+``mx.quantize`` rounding, MLX qmv's accumulation order, the native combine's
+bf16 ``sum`` order, ``mx.argpartition`` order inside tie sets, and mxfp4
+versus MLX (the OCP MX closed form is pinned).
 """
 
 from __future__ import annotations
