@@ -204,22 +204,22 @@ typedef struct zmoe_layer_desc {
  * Where ZMOE_LAYER_TRACE stamps land: byte offset into the workspace of a
  * uint64 array [n_blocks][n_slots] of 100 MHz realtime-counter values, one
  * row per workgroup, slots 0..12 = kernel start, router partials done,
- * barrier 1 passed, logits assembled, token 0 routed, units built, first
- * gate/up item done, gate/up done, down prefetch issued, barrier 2 passed,
- * act staged, down done, combine done; slots 13/14 = shader-clock counter at
+ * x staged, router logits received, token 0 routed, units built, first
+ * gate/up batch done, gate/up done, down prefetch issued, phase-A LDS
+ * released, act rows received, down done, combine done; slots 13/14 =
+ * shader-clock counter at
  * start / end.  Returns 0 if the single-launch kernel does not apply.
  * No counterpart in the reference (its profiling is wall-clock only,
  * profile.py:22); used for performance analysis.
  */
 size_t zmoe_moe_layer_trace_info(const zmoe_layer_desc* desc, int B, int* n_blocks, int* n_slots);
 
-/* Bytes of device workspace zmoe_moe_layer needs for B tokens.  The first
- * 16 KiB hold the single-launch kernel's grid-barrier state (arrival
- * counters and per-workgroup generation numbers that only ever increase):
- * the workspace must be zero-filled once before its first use and that
- * block must not be written by anything else afterwards.  Bytes 128..131
- * hold a sticky error word: nonzero if a barrier wait timed out (the block
- * is then inconsistent; zero-fill the workspace again before reuse). */
+/* Bytes of device workspace zmoe_moe_layer needs for B tokens.  The
+ * workspace belongs to one (desc, B): zero-fill it once before its first use
+ * and do not write it otherwise.  The single-launch kernel keeps a launch
+ * count per workgroup in it and tags the data its workgroups exchange with
+ * that count.  Bytes 128..131 hold a sticky error word: nonzero if a wait for
+ * exchanged data timed out (zero-fill the workspace again before reuse). */
 size_t zmoe_moe_layer_workspace_size(const zmoe_layer_desc* desc, int B);
 
 /*

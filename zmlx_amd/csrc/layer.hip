@@ -92,11 +92,16 @@ static bool use_fused(const zmoe_layer_desc* d, int B) {
   return forced == 1 && !(d->flags & ZMOE_LAYER_FORCE_MULTI) && fused_supported(d, B);
 }
 
+// The kernel sequence's buffers start after the single-launch kernel's (so
+// that data it leaves behind can never be mistaken for tagged data).
+static size_t multi_ws_offset(const zmoe_layer_desc* d, int B) {
+  const size_t fused = fused_supported(d, B) ? fused_workspace_bytes(d, B) : kSyncBlockBytes;
+  return (fused + 255) & ~static_cast<size_t>(255);
+}
+
 extern "C" size_t zmoe_moe_layer_workspace_size(const zmoe_layer_desc* desc, int B) {
   if (!desc || B < 0) return 0;
-  const size_t multi = layout_ws(desc, B, nullptr).bytes;
-  const size_t fused = fused_supported(desc, B) ? fused_workspace_bytes(desc, B) : 0;
-  return (kSyncBlockBytes + multi > fused) ? kSyncBlockBytes + multi : fused;
+  return multi_ws_offset(desc, B) + layout_ws(desc, B, nullptr).bytes;
 }
 
 extern "C" size_t zmoe_moe_layer_trace_info(const zmoe_layer_desc* desc, int B, int* n_blocks, int* n_slots) {
@@ -115,8 +120,8 @@ extern "C" int zmoe_moe_layer(void* stream, const zmoe_layer_desc* d, const void
   if (use_fused(d, B)) {
     return launch_fused(as_stream(stream), d, x, B, out, out_idx, out_w, workspace);
   }
-  // multi-kernel sequence: its buffers start after the barrier-state block
-  LayerWs ws = layout_ws(d, B, static_cast<char*>(workspace) + kSyncBlockBytes);
+  // multi-kernel sequence: its buffers follow the single-launch kernel's
+  LayerWs ws = layout_ws(d, B, static_cast<char*>(workspace) + multi_ws_offset(d, B));
   ZMOE_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(workspace) & 255) == 0,
                ZMOE_EINVAL_SHAPE, "[moe_layer] x must be 16-byte and workspace 256-byte aligned.");
   hipStream_t st = as_stream(stream);

@@ -1,44 +1,40 @@
 // Single-launch MoE decode layer (the fused path of zmoe_moe_layer).
 //
 // One persistent grid of G = (#CUs) workgroups x 8 waves, every workgroup
-// resident at once, runs the whole block in four phases separated by two
-// grid barriers:
+// resident at once, runs the whole block:
 //
 //   R  router projection: the E x (H/512) (row, 1 KiB chunk) units are
 //      spread over all waves; partial dots go to the workspace; meanwhile
 //      x is staged in LDS.
-//      -- barrier 1 --
-//   T  routing: every workgroup reduces the partials in a fixed order and
-//      routes each token (wave b <-> token b) -- redundantly, which is
-//      cheaper than a third barrier -- then gives the selected experts
-//      (plus the shared expert) unit slots.
+//   T  routing: every workgroup waits for the partials, reduces them in a
+//      fixed order and routes each token (wave b <-> token b) -- redundantly,
+//      which is cheaper than another grid-wide exchange -- then gives the
+//      selected experts (plus the shared expert) unit slots.
 //   A  gate/up + SwiGLU: rows of the units are spread over all waves; act
-//      rows go to the workspace.  Each wave then issues its first batch of
-//      down-projection weight loads *before* waiting, so that stream
-//      overlaps the barrier.
-//      -- barrier 2 --
-//   D  down projection: each wave owns output rows h for all units, so the
-//      k-ordered combine and the shared-expert add happen in-workgroup and
-//      each output element is written once.
+//      rows go to the workspace.  The waves' first batch of down-projection
+//      weight loads is issued together with the gate/up loads.
+//   D  down projection: each workgroup waits for the act rows; each wave
+//      owns output rows h for all units, so the k-ordered combine and the
+//      shared-expert add happen in-workgroup and each output is written once.
+//
+// Cross-workgroup data carries its own readiness: every router partial and
+// every act element is stored together with the launch's generation tag in
+// one device-scope atomic word (f32 | tag<<32, bf16 | tag<<16), and readers
+// poll until every tag they need is current.  There is no grid barrier: a
+// reader waits exactly for the data it consumes, and writers never wait for
+// their stores.  Each element is written once per launch and launches on a
+// stream do not overlap, so a current tag proves the value.  The tag is
+// 1 + the number of launches this workgroup completed on the workspace (kept
+// in the workspace, one word per workgroup; every workgroup runs every
+// launch, so all agree).  Every wait is bounded (on timeout: sticky error
+// word, continue), so the grid always drains.
 //
 // Code size matters here: the kernel runs each phase once per wave, so it is
 // written with rolled loops (per-token accumulators live in LDS) to stay
-// within the instruction cache.  Cross-workgroup data (router partials,
-// act rows, barrier words) use device-scope atomic accesses, which are
-// coherent across the XCDs without cache-wide writeback/invalidate.
-//
-// Grid barrier: workgroup g adds 1 (no return value) to arrival counter
-// g % 32, spreading same-address atomics over 32 lines; wave 0 of
-// workgroup 0 polls the 32 counters and then writes the generation number
-// to 8 release words, which the workgroups poll (g % 8).  Counters and
-// generations only increase (generation = 2 x launches so far + barrier
-// index, each workgroup keeps its launch count), so nothing is reset.
-// Waves wait only for their own stores before arriving and order LDS-only
-// within the workgroup, so weight prefetches stay in flight across a
-// barrier.  Every wait is bounded (on timeout: sticky error word,
-// continue), so the grid always drains.  The arithmetic is the multi-kernel path's (same dot
-// products, reduction trees, routing code and combine): results are
-// bit-identical to it.
+// within the instruction cache; one-token decode at H = 2048 has a
+// register-resident fast path.  The arithmetic is the multi-kernel path's
+// (same dot products, reduction trees, routing code and combine): results
+// are bit-identical to it.
 #include "zmoe_common.h"
 #include "zmoe_combine.h"
 #include "zmoe_host.h"
@@ -51,17 +47,12 @@ constexpr int kFWaves = kFThreads / kWave;
 constexpr int kFMaxB = 8;                 // tokens per call on the fused path
 constexpr int kFMaxUnits = kFMaxB * kMaxTopK + 1;
 constexpr int kChunkA = 4;                // (row-group, segment) items per batch, phase A
-constexpr int kChunkD = 8;                // (slot-group, segment) items per batch, phase D
+constexpr int kChunkD = 4;                // (slot-group, segment) items per batch, phase D
 constexpr unsigned kSpinLimit = 1u << 21;
 constexpr int kTraceSlots = 16;
-constexpr int kBarCtrs = 32;              // arrival counters
-constexpr int kBarRel = 8;                // release words
-constexpr int kLineWords = 32;            // 128-byte line, in uint32 words
-// barrier-state words at the start of the workspace
+// words of the workspace's leading state block
 constexpr int kErrWord = static_cast<int>(kSyncErrorByte / 4);
-constexpr int kCtrWord = 64;
-constexpr int kRelWord = kCtrWord + kBarCtrs * kLineWords;
-constexpr int kEpochWord = kRelWord + kBarRel * kLineWords;  // + workgroup
+constexpr int kEpochWord = 64;  // + workgroup: launches completed
 constexpr int kMaxGrid = static_cast<int>(kSyncBlockBytes / 4) - kEpochWord;
 constexpr int kMaxNC = 16;                // router chunks of 512 (H <= 8192)
 
@@ -76,9 +67,9 @@ struct FusedParams {
   const uint32_t* w[6];  // gate, up, down, sh_gate, sh_up, sh_down
   const void* s[6];
   const void* b[6];
-  unsigned* sync;        // barrier-state block (words kErrWord, kCtrWord, ...)
-  float* rpart;          // [B][E][NC]
-  uint16_t* act;         // [B*K + B][act_stride] bf16
+  unsigned* sync;        // state block (words kErrWord, kEpochWord + g)
+  unsigned long long* rpart;  // [B][E][NC]: f32 bits | tag << 32
+  uint32_t* act;         // [B*K + B][act_stride]: bf16 bits | (tag & 0xFFFF) << 16
   int act_stride;
   uint32_t* out_idx;
   float* out_w;
@@ -98,47 +89,49 @@ __device__ __forceinline__ void trace_mark(const FusedParams& p, int slot) {
   if (p.trace && threadIdx.x == 0) gstore(p.trace + blockIdx.x * kTraceSlots + slot, static_cast<unsigned long long>(wall_clock64()));
 }
 
-// Arrival at a grid barrier.  Precondition: every wave of the workgroup
-// has waited for its own device-scope stores and then passed lds_barrier().
-__device__ __forceinline__ void bar_arrive(const FusedParams& p) {
-  if (threadIdx.x == 0)
-    (void)__hip_atomic_fetch_add((ZMOE_GLOBAL unsigned*)(p.sync + kCtrWord + (blockIdx.x % kBarCtrs) * kLineWords),
-                                 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void bar_timeout(const FusedParams& p) {
+__device__ __forceinline__ void wait_timeout(const FusedParams& p) {
   __hip_atomic_fetch_or((ZMOE_GLOBAL unsigned*)(p.sync + kErrWord), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Wait for generation `gen` (every workgroup arrived `gen` times in total).
-__device__ void bar_wait(const FusedParams& p, unsigned gen) {
-  if (blockIdx.x == 0 && threadIdx.x < kWave) {
-    const unsigned G = gridDim.x;
-    const unsigned c = threadIdx.x;
-    const unsigned per = c < kBarCtrs ? G / kBarCtrs + (c < G % kBarCtrs ? 1u : 0u) : 0u;
-    const unsigned target = gen * per;  // modulo 2^32, compared by difference
-    unsigned n = 0;
-    for (;;) {
-      const bool ok = c >= kBarCtrs || static_cast<int>(dev_load(p.sync + kCtrWord + c * kLineWords) - target) >= 0;
-      if (__all(ok)) break;
-      if (++n > kSpinLimit) {
-        if (c == 0) bar_timeout(p);
-        break;
+// Router logits of one token, lane-strided (e = lane + 64 i): the H/512
+// partials of each expert, summed in chunk order once every one of them
+// carries `tag`, rounded to bf16 (the gate Linear returns bf16 logits).
+template <int P>
+__device__ __forceinline__ RowVals<P> poll_logits(const FusedParams& p, const unsigned long long* rp, int NC,
+                                                  unsigned tag) {
+  const int lane = __lane_id();
+  RowVals<P> row;
+  unsigned n = 0;
+  for (;;) {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      const int e = lane + 64 * i;
+      if (e < p.E) {
+        unsigned long long part[kMaxNC];
+#pragma unroll
+        for (int c = 0; c < kMaxNC; ++c)
+          if (c < NC) part[c] = dev_load(rp + e * NC + c);
+        float a = 0.0f;
+#pragma unroll
+        for (int c = 0; c < kMaxNC; ++c) {
+          if (c < NC) {
+            ok = ok && static_cast<unsigned>(part[c] >> 32) == tag;
+            a += __uint_as_float(static_cast<uint32_t>(part[c]));  // chunks in order
+          }
+        }
+        row.v[i] = round_bf16(a);
+      } else {
+        row.v[i] = -INFINITY;
       }
     }
-    if (c < kBarRel) dev_store(p.sync + kRelWord + c * kLineWords, gen);
-  }
-  if (threadIdx.x == 0) {
-    const unsigned* rel = p.sync + kRelWord + (blockIdx.x % kBarRel) * kLineWords;
-    unsigned n = 0;
-    while (static_cast<int>(dev_load(rel) - gen) < 0) {
-      if (++n > kSpinLimit) {
-        bar_timeout(p);
-        break;
-      }
+    if (__all(ok)) break;
+    if (++n > kSpinLimit) {
+      if (lane == 0) wait_timeout(p);
+      break;
     }
   }
-  lds_barrier();
+  return row;
 }
 
 // bf16 rows -> LDS tile in the layout of qmv.hip (stage_x_row):
@@ -146,8 +139,8 @@ __device__ void bar_wait(const FusedParams& p, unsigned gen) {
 // DEV: read the rows with device-coherent 64-bit loads (rows written by
 // other workgroups in this launch).
 template <int QMODE, bool DEV>
-__device__ __forceinline__ void stage_rows_lds(const uint16_t* __restrict__ src, int64_t src_stride, int nrows, int S,
-                                               uint32_t* xs, float* sx) {
+__device__ __forceinline__ void stage_rows_lds(const FusedParams& p, const void* __restrict__ src, int64_t src_stride,
+                                               int nrows, int S, uint32_t* xs, float* sx, unsigned tag16) {
   // all (row, segment, quarter) items at once, two per thread per round, so
   // the loads of every row are in flight together
   const int S4 = S * 4;
@@ -158,16 +151,33 @@ __device__ __forceinline__ void stage_rows_lds(const uint16_t* __restrict__ src,
     for (int h = 0; h < 2; ++h) {
       const int i = i0 + h * kFThreads;
       if (i < n) {
-        const int r = i / S4, rem = i - r * S4;
-        const uint16_t* q16 = src + r * src_stride + rem * 8;  // segment rem>>2, quarter rem&3
+        const int r = i / S4, rem = i - r * S4;  // segment rem>>2, quarter rem&3
         if (DEV) {
-          const unsigned long long* q = reinterpret_cast<const unsigned long long*>(q16);
-          const unsigned long long lo = dev_load(q);
-          const unsigned long long hi = dev_load(q + 1);
-          v[h] = make_uint4(static_cast<uint32_t>(lo), static_cast<uint32_t>(lo >> 32), static_cast<uint32_t>(hi),
-                            static_cast<uint32_t>(hi >> 32));
+          // 8 tagged words (bf16 | tag<<16), polled until all are current
+          const unsigned long long* q =
+              reinterpret_cast<const unsigned long long*>(static_cast<const uint32_t*>(src) + r * src_stride + rem * 8);
+          const unsigned long long want = (static_cast<unsigned long long>(tag16) << 48) | (tag16 << 16);
+          const unsigned long long tmask = 0xFFFF0000FFFF0000ull;
+          unsigned long long w0, w1, w2, w3;
+          unsigned n = 0;
+          for (;;) {
+            w0 = dev_load(q);
+            w1 = dev_load(q + 1);
+            w2 = dev_load(q + 2);
+            w3 = dev_load(q + 3);
+            if (((w0 & tmask) == want) && ((w1 & tmask) == want) && ((w2 & tmask) == want) && ((w3 & tmask) == want))
+              break;
+            if (++n > kSpinLimit) {
+              wait_timeout(p);
+              break;
+            }
+          }
+          auto pair = [](unsigned long long w) {
+            return static_cast<uint32_t>(w & 0xFFFFu) | static_cast<uint32_t>((w >> 16) & 0xFFFF0000u);
+          };
+          v[h] = make_uint4(pair(w0), pair(w1), pair(w2), pair(w3));
         } else {
-          v[h] = gload(reinterpret_cast<const uint4*>(q16));
+          v[h] = gload(reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(src) + r * src_stride + rem * 8));
         }
       }
     }
@@ -210,28 +220,12 @@ __device__ __forceinline__ void stage_rows_lds(const uint16_t* __restrict__ src,
 }
 
 template <int QMODE>
-__device__ __forceinline__ float seg_dot_lds(const uint4 w, const uint32_t* xs, int S, int r, int s) {
+__device__ __forceinline__ float seg_dot_lds(const uint4 w, const uint32_t* xs, int S, int r, int s, AffineK k) {
   const uint4 x0 = *reinterpret_cast<const uint4*>(xs + ((r * 4 + 0) * S + s) * 4);
   const uint4 x1 = *reinterpret_cast<const uint4*>(xs + ((r * 4 + 1) * S + s) * 4);
   const uint4 x2 = *reinterpret_cast<const uint4*>(xs + ((r * 4 + 2) * S + s) * 4);
   const uint4 x3 = *reinterpret_cast<const uint4*>(xs + ((r * 4 + 3) * S + s) * 4);
-  const uint32_t a0[4] = {x0.x, x0.y, x0.z, x0.w};
-  const uint32_t a1[4] = {x1.x, x1.y, x1.z, x1.w};
-  const uint32_t a2[4] = {x2.x, x2.y, x2.z, x2.w};
-  const uint32_t a3[4] = {x3.x, x3.y, x3.z, x3.w};
-  float v = 0.0f;
-  if (QMODE == ZMOE_Q_AFFINE) {
-    v = dot_affine4_word(w.x, a0, v);
-    v = dot_affine4_word(w.y, a1, v);
-    v = dot_affine4_word(w.z, a2, v);
-    v = dot_affine4_word(w.w, a3, v);
-  } else {
-    v = dot_mxfp4_word(w.x, a0, v);
-    v = dot_mxfp4_word(w.y, a1, v);
-    v = dot_mxfp4_word(w.z, a2, v);
-    v = dot_mxfp4_word(w.w, a3, v);
-  }
-  return v;
+  return seg_dot<QMODE>(w, x0, x1, x2, x3, k);
 }
 
 // Quantisation parameters of one (row, segment): loaded raw, decoded at use
@@ -308,11 +302,14 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
   const int E = p.E;
   const int NC = p.H >> 9;
   const int S_H = p.H >> 5, S_I = p.I >> 5;
+  const AffineK ak = affine_k();
   const bool has_shared = p.Is > 0;
   trace_mark(p, 0);
   if (p.trace && threadIdx.x == 0) gstore(p.trace + blockIdx.x * kTraceSlots + 13, static_cast<unsigned long long>(clock64()));
   // launches this workgroup completed before (written by itself only)
-  const unsigned epoch = wave == 0 ? dev_load(p.sync + kEpochWord + blockIdx.x) : 0u;
+  const unsigned epoch = dev_load(p.sync + kEpochWord + blockIdx.x);
+  const unsigned tag = epoch + 1u;
+  const unsigned tag16 = tag & 0xFFFFu;
 
   // phase R..A LDS: x tile, x sums, grouped-router scratch, accumulators
   uint32_t* xs = reinterpret_cast<uint32_t*>(big);
@@ -332,36 +329,22 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
       a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv.z), __builtin_bit_cast(bf16x2_t, xv.z), a, false);
       a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv.w), __builtin_bit_cast(bf16x2_t, xv.w), a, false);
       a = wave_sum(a);
-      if (lane == 0) dev_store(p.rpart + (static_cast<int64_t>(b) * E + e) * NC + c, a);
+      if (lane == 0)
+        dev_store(p.rpart + (static_cast<int64_t>(b) * E + e) * NC + c,
+                  (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(a));
     }
   }
-  stage_rows_lds<QMODE, false>(p.x, p.H, B, S_H, xs, sx);
+  stage_rows_lds<QMODE, false>(p, p.x, p.H, B, S_H, xs, sx, 0u);
   trace_mark(p, 1);
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's partials are stored
   lds_barrier();
-  bar_arrive(p);
-  bar_wait(p, 2 * epoch + 1);
   trace_mark(p, 2);
 
   // ---------------- phase T: routing (wave b <-> token b) ----------------
   if (wave < B) {
     const int b = wave;
-    const float* rp = p.rpart + static_cast<int64_t>(b) * E * NC;
+    const RowVals<P> row = poll_logits<P>(p, p.rpart + static_cast<int64_t>(b) * E * NC, NC, tag);
     trace_mark(p, 3);
-    route_row_p<P>(
-        p.route,
-        [&](int e) {
-          float part[kMaxNC];
-#pragma unroll
-          for (int c = 0; c < kMaxNC; ++c)
-            if (c < NC) part[c] = dev_load(rp + e * NC + c);
-          float a = 0.0f;
-#pragma unroll
-          for (int c = 0; c < kMaxNC; ++c)
-            if (c < NC) a += part[c];  // chunks in order
-          return round_bf16(a);        // the gate Linear returns bf16 logits
-        },
-        *(ZMOE_LDS RouteLds*)(&L.route[b]), (ZMOE_LDS float*)(rv + static_cast<size_t>(b) * E));
+    route_row<P>(p.route, row, *(ZMOE_LDS RouteLds*)(&L.route[b]), (ZMOE_LDS float*)(rv + static_cast<size_t>(b) * E));
     trace_mark(p, 4);
     if (blockIdx.x == 0 && lane < p.K) {
       if (p.out_idx) gstore(p.out_idx + b * p.K + lane, static_cast<uint32_t>(L.route[b].sel[lane]));
@@ -405,8 +388,151 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
   const int Uall = U + (has_shared ? 1 : 0);
   trace_mark(p, 5);
 
+  // ---------------- phase D setup ----------------
+  // The first batch of down-projection weight loads is issued during phase A,
+  // once the wave's gate/up data has arrived.
+  // This wave owns output rows [h0, h0 + nrows); slot = (row, unit) with the
+  // unit fastest; RPID slots per load instruction, lane group rsD.
+  const int LI = p.LI, RPID = kWave / LI;
+  const int rsD = lane / LI, liD = lane & (LI - 1);
+  const int TD = S_I / LI;
+  const int rows_per_wave = (p.H + W - 1) / W;
+  const int h0 = gw * rows_per_wave;
+  const int nrows = max(0, min(p.H, h0 + rows_per_wave) - h0);
+  const int slots = nrows * Uall;
+  const int n_groups = (slots + RPID - 1) / RPID;
+  const int n_itemsD = n_groups * TD;
+  const int64_t wprD = p.I >> 3;
+  const int64_t pprD = (QMODE == ZMOE_Q_AFFINE) ? (S_I >> p.gshift) : S_I;
+  // per-lane slot cursor (row hl, unit uu) and segment cursor (wave-uniform)
+  int d_hl = rsD / max(Uall, 1), d_u = rsD - d_hl * Uall, d_t = 0, d_g = 0;
+  uint4 wd[kChunkD];
+  RawParam rd[kChunkD];
+  int jhl[kChunkD], ju[kChunkD], jt[kChunkD], jvalid[kChunkD];
+  // Loads are unconditional, so the waits of phase A can count them: items
+  // past the end repeat the previous item's addresses (a cache hit), or read
+  // x if the wave has no down work.
+  bool d_issued = false;
+  auto load_down_batch = [&](int base) {
+    const uint32_t* wp = reinterpret_cast<const uint32_t*>(p.x);
+    const void* sp = p.x;
+    const void* bp = p.x;
+    int64_t poff = 0;
+#pragma unroll
+    for (int j = 0; j < kChunkD; ++j) {
+      jhl[j] = min(d_hl, nrows - 1);
+      ju[j] = d_u;
+      jt[j] = d_t;
+      jvalid[j] = d_g * RPID + rsD < slots;
+      if (base + j < n_itemsD) {
+        const UnitPtr pd = unit_ptr<QMODE>(p, L, d_u, 2);
+        const int s = d_t * LI + liD;
+        const int64_t row = h0 + jhl[j];
+        wp = pd.w + row * wprD + s * 4;
+        sp = pd.s;
+        bp = pd.b;
+        poff = row * pprD + ((QMODE == ZMOE_Q_AFFINE) ? (s >> p.gshift) : s);
+        if (++d_t == TD) {  // next slot-group: advance this lane's slot by RPID
+          d_t = 0;
+          ++d_g;
+          d_u += RPID;
+          while (d_u >= Uall) {
+            d_u -= Uall;
+            ++d_hl;
+          }
+          d_u = (d_hl >= nrows) ? 0 : d_u;  // past the end: any valid unit (result unused)
+        }
+      }
+      wd[j] = gload(reinterpret_cast<const uint4*>(wp));
+      rd[j] = seg_param_load<QMODE>(sp, bp, poff);
+    }
+    d_issued = true;
+  };
+
   // ---------------- phase A: gate/up + SwiGLU ----------------
-  {
+  if (B == 1 && S_H == kWave) {
+    // One token, H = 2048: lane l owns x segment l of every row, so the x
+    // segment and the per-row accumulators stay in registers; loads are
+    // issued unconditionally (past the end they repeat the previous item's
+    // addresses, a cache hit) so each item waits only for its own data.
+    const int rg_total = Uall * p.I;
+    const int per = (rg_total + W - 1) / W;
+    const int g0 = min(rg_total, gw * per), g1 = min(rg_total, g0 + per);
+    const uint4 x0 = *reinterpret_cast<const uint4*>(xs + ((0 * 4 + 0) * S_H + lane) * 4);
+    const uint4 x1 = *reinterpret_cast<const uint4*>(xs + ((0 * 4 + 1) * S_H + lane) * 4);
+    const uint4 x2 = *reinterpret_cast<const uint4*>(xs + ((0 * 4 + 2) * S_H + lane) * 4);
+    const uint4 x3 = *reinterpret_cast<const uint4*>(xs + ((0 * 4 + 3) * S_H + lane) * 4);
+    const float xsum = (QMODE == ZMOE_Q_AFFINE) ? sx[lane] : 0.0f;
+    const int64_t wpr = p.H >> 3;
+    const int64_t ppr = (QMODE == ZMOE_Q_AFFINE) ? (S_H >> p.gshift) : S_H;
+    const int pi = (QMODE == ZMOE_Q_AFFINE) ? (lane >> p.gshift) : lane;
+    int cu_unit = g0 / p.I;
+    int cu_row = g0 - cu_unit * p.I;
+    for (int base = g0; base < g1; base += kChunkA) {
+      uint4 wg[kChunkA], wu[kChunkA];
+      RawParam rg[kChunkA], ru[kChunkA];
+      int jrow[kChunkA], jpair[kChunkA];
+      const uint32_t *gwp = nullptr, *uwp = nullptr;
+      const void *gsp = nullptr, *gbp = nullptr, *usp = nullptr, *ubp = nullptr;
+      int64_t poff = 0;
+#pragma unroll
+      for (int j = 0; j < kChunkA; ++j) {
+        if (j == 0 || base + j < g1) {
+          const UnitPtr pg = unit_ptr<QMODE>(p, L, cu_unit, 0);
+          const UnitPtr pu = unit_ptr<QMODE>(p, L, cu_unit, 1);
+          gwp = pg.w + cu_row * wpr + lane * 4;
+          uwp = pu.w + cu_row * wpr + lane * 4;
+          gsp = pg.s;
+          gbp = pg.b;
+          usp = pu.s;
+          ubp = pu.b;
+          poff = cu_row * ppr + pi;
+          jrow[j] = cu_row;
+          jpair[j] = L.upairs[cu_unit][0];
+          if (++cu_row == p.I) {
+            cu_row = 0;
+            ++cu_unit;
+          }
+        } else {
+          jrow[j] = jrow[j - 1];
+          jpair[j] = jpair[j - 1];
+        }
+        wg[j] = gload(reinterpret_cast<const uint4*>(gwp));
+        wu[j] = gload(reinterpret_cast<const uint4*>(uwp));
+        rg[j] = seg_param_load<QMODE>(gsp, gbp, poff);
+        ru[j] = seg_param_load<QMODE>(usp, ubp, poff);
+      }
+      float gv[kChunkA], uv[kChunkA];
+#pragma unroll
+      for (int j = 0; j < kChunkA; ++j) {
+        float sg, cg, su, cu;
+        seg_param_decode<QMODE>(rg[j], sg, cg);
+        seg_param_decode<QMODE>(ru[j], su, cu);
+        gv[j] = wave_sum(seg_accum<QMODE>(0.0f, sg, cg, seg_dot<QMODE>(wg[j], x0, x1, x2, x3, ak), xsum));
+        uv[j] = wave_sum(seg_accum<QMODE>(0.0f, su, cu, seg_dot<QMODE>(wu[j], x0, x1, x2, x3, ak), xsum));
+      }
+      if (base == g0) trace_mark(p, 6);
+      // lane j finalises item j (every lane holds every item's sums)
+      float gsel = gv[0], usel = uv[0];
+      int rsel = jrow[0], psel = jpair[0];
+#pragma unroll
+      for (int j = 1; j < kChunkA; ++j) {
+        if (lane == j) {
+          gsel = gv[j];
+          usel = uv[j];
+          rsel = jrow[j];
+          psel = jpair[j];
+        }
+      }
+      if (lane < kChunkA && base + lane < g1)
+        dev_store(p.act + static_cast<int64_t>(psel) * p.act_stride + rsel,
+                  (tag16 << 16) | swiglu_bf16(round_bf16(gsel), round_bf16(usel)));
+      // gate/up data is in and the act rows are on their way: start the down
+      // stream (issued earlier it would compete with this phase's loads and
+      // hold the stores back)
+      if (base == g0) load_down_batch(0);
+    }
+  } else {
     const int LH = p.LH, RPI = kWave / LH;
     const int rs = lane / LH, li = lane & (LH - 1);
     const int T = S_H / LH;
@@ -466,8 +592,8 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
             const float xsum = (QMODE == ZMOE_Q_AFFINE) ? sx[b * S_H + s] : 0.0f;
             const float g_prev = t == 0 ? 0.0f : ag[tk * kWave];
             const float u_prev = t == 0 ? 0.0f : au[tk * kWave];
-            ag[tk * kWave] = seg_accum<QMODE>(g_prev, sgj, cgj, seg_dot_lds<QMODE>(wg[j], xs, S_H, b, s), xsum);
-            au[tk * kWave] = seg_accum<QMODE>(u_prev, suj, cuj, seg_dot_lds<QMODE>(wu[j], xs, S_H, b, s), xsum);
+            ag[tk * kWave] = seg_accum<QMODE>(g_prev, sgj, cgj, seg_dot_lds<QMODE>(wg[j], xs, S_H, b, s, ak), xsum);
+            au[tk * kWave] = seg_accum<QMODE>(u_prev, suj, cuj, seg_dot_lds<QMODE>(wu[j], xs, S_H, b, s, ak), xsum);
           }
           if (base == 0 && j == 0) trace_mark(p, 6);
           if (t == T - 1) {  // row-group complete: reduce, SwiGLU, store act
@@ -475,8 +601,8 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
               const float gv = lanes_sum(ag[tk * kWave], LH);
               const float uv = lanes_sum(au[tk * kWave], LH);
               if (li == 0)
-                dev_store<uint16_t>(p.act + static_cast<int64_t>(L.upairs[u][tk]) * p.act_stride + irow[j],
-                              static_cast<uint16_t>(swiglu_bf16(round_bf16(gv), round_bf16(uv))));
+                dev_store(p.act + static_cast<int64_t>(L.upairs[u][tk]) * p.act_stride + irow[j],
+                          (tag16 << 16) | swiglu_bf16(round_bf16(gv), round_bf16(uv)));
             }
           }
         }
@@ -485,58 +611,9 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
   }
   trace_mark(p, 7);
 
-  // ---------------- phase D setup: first down batch before the barrier ----------------
-  // This wave owns output rows [h0, h0 + nrows); slot = (row, unit) with the
-  // unit fastest; RPID slots per load instruction, lane group rsD.
-  const int LI = p.LI, RPID = kWave / LI;
-  const int rsD = lane / LI, liD = lane & (LI - 1);
-  const int TD = S_I / LI;
-  const int rows_per_wave = (p.H + W - 1) / W;
-  const int h0 = gw * rows_per_wave;
-  const int nrows = max(0, min(p.H, h0 + rows_per_wave) - h0);
-  const int slots = nrows * Uall;
-  const int n_groups = (slots + RPID - 1) / RPID;
-  const int n_itemsD = n_groups * TD;
-  const int64_t wprD = p.I >> 3;
-  const int64_t pprD = (QMODE == ZMOE_Q_AFFINE) ? (S_I >> p.gshift) : S_I;
-  // per-lane slot cursor (row hl, unit uu) and segment cursor (wave-uniform)
-  int d_hl = rsD / max(Uall, 1), d_u = rsD - d_hl * Uall, d_t = 0, d_g = 0;
-  uint4 wd[kChunkD];
-  RawParam rd[kChunkD];
-  int jhl[kChunkD], ju[kChunkD], jt[kChunkD], jvalid[kChunkD];
-  auto load_down_batch = [&](int base) {
-#pragma unroll
-    for (int j = 0; j < kChunkD; ++j) {
-      jhl[j] = min(d_hl, nrows - 1);
-      ju[j] = d_u;
-      jt[j] = d_t;
-      jvalid[j] = d_g * RPID + rsD < slots;
-      if (base + j < n_itemsD) {
-        const UnitPtr pd = unit_ptr<QMODE>(p, L, d_u, 2);
-        const int s = d_t * LI + liD;
-        const int64_t row = h0 + jhl[j];
-        wd[j] = gload(reinterpret_cast<const uint4*>(pd.w + row * wprD + s * 4));
-        const int pi = (QMODE == ZMOE_Q_AFFINE) ? (s >> p.gshift) : s;
-        rd[j] = seg_param_load<QMODE>(pd.s, pd.b, row * pprD + pi);
-        if (++d_t == TD) {  // next slot-group: advance this lane's slot by RPID
-          d_t = 0;
-          ++d_g;
-          d_u += RPID;
-          while (d_u >= Uall) {
-            d_u -= Uall;
-            ++d_hl;
-          }
-          d_u = (d_hl >= nrows) ? 0 : d_u;  // past the end: any valid unit (result unused)
-        }
-      }
-    }
-  };
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's act rows are stored
-  load_down_batch(0);             // stays in flight across the barrier
+  if (!d_issued) load_down_batch(0);
   trace_mark(p, 8);
-  lds_barrier();
-  bar_arrive(p);
-  bar_wait(p, 2 * epoch + 2);
+  lds_barrier();  // the workgroup is done with the phase A tiles (aliased below)
   trace_mark(p, 9);
 
   // ---------------- phase D: down projection ----------------
@@ -546,7 +623,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
   float* asx = reinterpret_cast<float*>(as + static_cast<size_t>(Ptot) * S_I * 16);
   float* ybuf = asx + static_cast<size_t>(Ptot) * S_I;                         // [wg rows][Ptot]
   float* accD = ybuf + static_cast<size_t>(kFWaves) * rows_per_wave * Ptot;   // [waves][B][64]
-  stage_rows_lds<QMODE, true>(p.act, p.act_stride, Ptot, S_I, as, asx);
+  stage_rows_lds<QMODE, true>(p, p.act, p.act_stride, Ptot, S_I, as, asx, tag16);
   lds_barrier();
   trace_mark(p, 10);
   float* ad = accD + static_cast<size_t>(wave) * B * kWave + lane;
@@ -564,7 +641,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
           const int q = L.upairs[u][tk];
           const float xsum = (QMODE == ZMOE_Q_AFFINE) ? asx[q * S_I + s] : 0.0f;
           const float prev = t == 0 ? 0.0f : ad[tk * kWave];
-          ad[tk * kWave] = seg_accum<QMODE>(prev, sdj, cdj, seg_dot_lds<QMODE>(wd[j], as, S_I, q, s), xsum);
+          ad[tk * kWave] = seg_accum<QMODE>(prev, sdj, cdj, seg_dot_lds<QMODE>(wd[j], as, S_I, q, s, ak), xsum);
         }
         if (t == TD - 1) {
           for (int tk = 0; tk < nt; ++tk) {
@@ -638,15 +715,15 @@ bool fused_supported(const zmoe_layer_desc* d, int B) {
   return true;
 }
 
-// workspace: barrier-state block | rpart | act | trace
+// workspace: state block | rpart | act | trace
 static size_t off_rpart() { return kSyncBlockBytes; }
 static size_t off_act(const zmoe_layer_desc* d, int B) {
-  return align256(off_rpart() + static_cast<size_t>(B) * d->n_experts * (d->hidden / 512) * 4);
+  return align256(off_rpart() + static_cast<size_t>(B) * d->n_experts * (d->hidden / 512) * 8);
 }
 static size_t off_trace(const zmoe_layer_desc* d, int B) {
   const int stride = d->inter > d->shared_inter ? d->inter : d->shared_inter;
   const size_t Ptot = static_cast<size_t>(B) * d->top_k + (d->shared_inter > 0 ? B : 0);
-  return align256(off_act(d, B) + Ptot * stride * 2);
+  return align256(off_act(d, B) + Ptot * stride * 4);
 }
 
 size_t fused_workspace_bytes(const zmoe_layer_desc* d, int B) {
@@ -724,8 +801,8 @@ int launch_fused(hipStream_t st, const zmoe_layer_desc* d, const void* x, int B,
   }
   char* base = static_cast<char*>(workspace);
   fp.sync = reinterpret_cast<unsigned*>(base);
-  fp.rpart = reinterpret_cast<float*>(base + off_rpart());
-  fp.act = reinterpret_cast<uint16_t*>(base + off_act(d, B));
+  fp.rpart = reinterpret_cast<unsigned long long*>(base + off_rpart());
+  fp.act = reinterpret_cast<uint32_t*>(base + off_act(d, B));
   fp.act_stride = d->inter > d->shared_inter ? d->inter : d->shared_inter;
   fp.out_idx = out_idx;
   fp.out_w = out_w;

@@ -54,29 +54,6 @@ __device__ void stage_x_row(const uint16_t* __restrict__ xrow, int S, uint32_t* 
   }
 }
 
-// Contribution of one 16-byte weight segment `w` against token data.
-template <int QMODE>
-__device__ __forceinline__ float seg_dot(const uint4 w, const uint4 x0, const uint4 x1, const uint4 x2,
-                                         const uint4 x3) {
-  const uint32_t a0[4] = {x0.x, x0.y, x0.z, x0.w};
-  const uint32_t a1[4] = {x1.x, x1.y, x1.z, x1.w};
-  const uint32_t a2[4] = {x2.x, x2.y, x2.z, x2.w};
-  const uint32_t a3[4] = {x3.x, x3.y, x3.z, x3.w};
-  float v = 0.0f;
-  if (QMODE == ZMOE_Q_AFFINE) {
-    v = dot_affine4_word(w.x, a0, v);
-    v = dot_affine4_word(w.y, a1, v);
-    v = dot_affine4_word(w.z, a2, v);
-    v = dot_affine4_word(w.w, a3, v);
-  } else {
-    v = dot_mxfp4_word(w.x, a0, v);
-    v = dot_mxfp4_word(w.y, a1, v);
-    v = dot_mxfp4_word(w.z, a2, v);
-    v = dot_mxfp4_word(w.w, a3, v);
-  }
-  return v;
-}
-
 // Per-(row, segment) quantisation parameters.
 struct SegParam {
   float s;  // scale
@@ -115,6 +92,7 @@ __device__ __forceinline__ void wave_qmv(const uint32_t* __restrict__ Wg, const 
   const int T = S / L;
   const int64_t wpr = K >> 3;                                        // words per row
   const int64_t ppr = (QMODE == ZMOE_Q_AFFINE) ? (S >> gshift) : S;  // params per row
+  const AffineK ak = affine_k();
 
   int64_t rowoff[J];
 #pragma unroll
@@ -153,10 +131,10 @@ __device__ __forceinline__ void wave_qmv(const uint32_t* __restrict__ Wg, const 
         const float xsum = (QMODE == ZMOE_Q_AFFINE) ? sx[tok * S + s] : 0.0f;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-          const float vg = seg_dot<QMODE>(wg[j], x0, x1, x2, x3);
+          const float vg = seg_dot<QMODE>(wg[j], x0, x1, x2, x3, ak);
           rg[j][tok] = seg_accum<QMODE>(rg[j][tok], pg[j].s, pg[j].c, vg, xsum);
           if (SWIGLU) {
-            const float vu = seg_dot<QMODE>(wu[j], x0, x1, x2, x3);
+            const float vu = seg_dot<QMODE>(wu[j], x0, x1, x2, x3, ak);
             ru[j][tok] = seg_accum<QMODE>(ru[j][tok], pu[j].s, pu[j].c, vu, xsum);
           }
         }

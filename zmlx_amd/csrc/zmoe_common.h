@@ -172,8 +172,24 @@ __device__ __forceinline__ float lanes_sum(float v, int L) {
 //    bits (q | 0x4300) are the bf16 number 128+q (exact for q < 128).
 // The dot2 therefore accumulates sum x*(128+q); the caller removes the
 // offset with the per-segment activation sum:  sum x*q = v - 128*sum x.
-__device__ __forceinline__ float dot_affine4_word(uint32_t w, const uint32_t xp[4], float acc) {
-  const uint32_t m = 0x000F000Fu, o = 0x43004300u;
+//
+// The mask and offset come in as registers (AffineK) so that each pair is one
+// v_and_or_b32 instead of an AND and an OR with literal operands.
+struct AffineK {
+  uint32_t m, o;
+};
+
+// 0x000F000F / 0x43004300 in registers the compiler cannot fold back into
+// literals (call once, outside the hot loop).
+__device__ __forceinline__ AffineK affine_k() {
+  AffineK k{0x000F000Fu, 0x43004300u};
+  asm("" : "+v"(k.m));
+  asm("" : "+v"(k.o));
+  return k;
+}
+
+__device__ __forceinline__ float dot_affine4_word(uint32_t w, const uint32_t xp[4], float acc, AffineK k) {
+  const uint32_t m = k.m, o = k.o;
   uint32_t a = (w & m) | o;
   uint32_t b = ((w >> 4) & m) | o;
   uint32_t c = ((w >> 8) & m) | o;
@@ -198,6 +214,30 @@ __device__ __forceinline__ float dot_mxfp4_word(uint32_t w, const uint32_t xp[4]
   acc = __builtin_amdgcn_fdot2_f32_bf16(p2, __builtin_bit_cast(bf16x2_t, xp[2]), acc, false);
   acc = __builtin_amdgcn_fdot2_f32_bf16(p3, __builtin_bit_cast(bf16x2_t, xp[3]), acc, false);
   return acc;
+}
+
+// Contribution of one 16-byte weight segment `w` against the matching 16
+// staged activation words x0..x3 (see the layouts above).
+template <int QMODE>
+__device__ __forceinline__ float seg_dot(const uint4 w, const uint4 x0, const uint4 x1, const uint4 x2,
+                                         const uint4 x3, AffineK k) {
+  const uint32_t a0[4] = {x0.x, x0.y, x0.z, x0.w};
+  const uint32_t a1[4] = {x1.x, x1.y, x1.z, x1.w};
+  const uint32_t a2[4] = {x2.x, x2.y, x2.z, x2.w};
+  const uint32_t a3[4] = {x3.x, x3.y, x3.z, x3.w};
+  float v = 0.0f;
+  if (QMODE == 0) {
+    v = dot_affine4_word(w.x, a0, v, k);
+    v = dot_affine4_word(w.y, a1, v, k);
+    v = dot_affine4_word(w.z, a2, v, k);
+    v = dot_affine4_word(w.w, a3, v, k);
+  } else {
+    v = dot_mxfp4_word(w.x, a0, v);
+    v = dot_mxfp4_word(w.y, a1, v);
+    v = dot_mxfp4_word(w.z, a2, v);
+    v = dot_mxfp4_word(w.w, a3, v);
+  }
+  return v;
 }
 
 // Accumulate one segment's contribution into `acc` with an explicit operation

@@ -152,7 +152,7 @@ class QuantizedMoELayer:
         ws = self._ws.get(B)
         if ws is None:
             # zero-filled once: the leading block holds the fused kernel's
-            # barrier state (counters that only increase from call to call)
+            # launch counts (they only increase from call to call)
             ws = torch.zeros(self.workspace_bytes(B), dtype=torch.uint8, device=self.device)
             self._ws[B] = ws
         return ws
@@ -198,7 +198,7 @@ class QuantizedMoELayer:
         return ws[off: off + 8 * n].view(torch.int64).reshape(nb.value, ns.value).clone()
 
     def sync_error(self) -> int:
-        """Sticky error word of the fused kernel's grid barriers (0 = ok)."""
+        """Sticky error word of the fused kernel's cross-workgroup waits (0 = ok)."""
         flags = 0
         for ws in self._ws.values():
             flags |= int(ws[128:132].view(torch.int32).item())
