@@ -124,6 +124,31 @@ constexpr int kDppQuadSwap2 = 0x4E;  // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141;
 constexpr int kDppRowMirror = 0x140;
 
+// Row-pair and half-wave exchanges (gfx950 v_permlane16/32_swap): with both
+// operands = v, result [0] holds the lower partner's value and [1] the
+// upper partner's in every lane, so  [0] op [1]  is the same expression in
+// both lanes of a pair.
+__device__ __forceinline__ float rows_combine_add(float v) {
+  const auto q = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                  false, false);
+  return __builtin_bit_cast(float, static_cast<uint32_t>(q[0])) + __builtin_bit_cast(float, static_cast<uint32_t>(q[1]));
+}
+__device__ __forceinline__ float halves_combine_add(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                  false, false);
+  return __builtin_bit_cast(float, static_cast<uint32_t>(r[0])) + __builtin_bit_cast(float, static_cast<uint32_t>(r[1]));
+}
+__device__ __forceinline__ float rows_combine_max(float v) {
+  const auto q = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                  false, false);
+  return fmaxf(__builtin_bit_cast(float, static_cast<uint32_t>(q[0])), __builtin_bit_cast(float, static_cast<uint32_t>(q[1])));
+}
+__device__ __forceinline__ float halves_combine_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                  false, false);
+  return fmaxf(__builtin_bit_cast(float, static_cast<uint32_t>(r[0])), __builtin_bit_cast(float, static_cast<uint32_t>(r[1])));
+}
+
 __device__ __forceinline__ float readlane_f(float v, int l) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
@@ -135,8 +160,10 @@ __device__ __forceinline__ float wave_sum_width(float v) {
   if (WIDTH >= 4) ZMOE_DPP_ADD(v, kDppQuadSwap2);
   if (WIDTH >= 8) ZMOE_DPP_ADD(v, kDppHalfMirror);
   if (WIDTH >= 16) ZMOE_DPP_ADD(v, kDppRowMirror);
-  if (WIDTH == 32) v += __shfl_xor(v, 16);
-  if (WIDTH == 64) v = (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
+  // rows (16 lanes) combined as (row0 + row1) + (row2 + row3); every lane
+  // ends with the sum of its WIDTH-lane group
+  if (WIDTH >= 32) v = rows_combine_add(v);
+  if (WIDTH == 64) v = halves_combine_add(v);
   return v;
 }
 
@@ -147,7 +174,7 @@ __device__ __forceinline__ float wave_max(float v) {
   ZMOE_DPP_MAX(v, kDppQuadSwap2);
   ZMOE_DPP_MAX(v, kDppHalfMirror);
   ZMOE_DPP_MAX(v, kDppRowMirror);
-  return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+  return halves_combine_max(rows_combine_max(v));
 }
 
 // Runtime group width L in {8, 16, 32, 64} (lanes sharing one weight row).

@@ -4,9 +4,10 @@
 //
 // Layout: lane l holds experts l, l+64, ... (P values per lane, P = 1..16
 // for E <= 64P) in registers; wave-private LDS holds only the short winner
-// list.  Top-k is a radix select of the k-th key on wave ballots (32 steps,
-// no memory traffic), then the winners are ranked.  Selection order
-// everywhere: value descending, lower expert index first on ties.
+// list.  Top-k is k rounds of wave argmax on order-preserving integer keys
+// (DPP max, then a ballot for the lowest index holding it), no memory
+// traffic.  Selection order everywhere: value descending, lower expert index
+// first on ties.
 #pragma once
 
 #include "zmoe_common.h"
@@ -18,11 +19,6 @@ constexpr int kMaxTopK = 16;
 // Per-wave LDS scratch of the router.
 struct RouteLds {
   float gsc[64];  // group scores (grouped router)
-  int cnt;        // winner list length
-  uint32_t wkey[kMaxTopK];
-  int widx[kMaxTopK];
-  float wval[kMaxTopK];
-  float waux[kMaxTopK];
   int sel[kMaxTopK];   // result: selected experts in order
   float sval[kMaxTopK];
   float saux[kMaxTopK];
@@ -66,57 +62,134 @@ __device__ __forceinline__ float reg_row_max(const float (&v)[P], int E) {
   return wave_max(m);
 }
 
-// k largest of v[0..n) (lane-strided registers), ties to the lower index.
-// Fills R.sel / R.sval (value) / R.saux (aux[] of the winner) in order
-// (value desc, index asc).  All 64 lanes call it.
+// Wave maximum of an unsigned key (every lane gets it).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#define ZMOE_DPP_UMAX(ctrl) \
+  v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), (ctrl), 0xF, 0xF, false)))
+  ZMOE_DPP_UMAX(kDppQuadSwap1);
+  ZMOE_DPP_UMAX(kDppQuadSwap2);
+  ZMOE_DPP_UMAX(kDppHalfMirror);
+  ZMOE_DPP_UMAX(kDppRowMirror);
+#undef ZMOE_DPP_UMAX
+  const auto q = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max(static_cast<uint32_t>(q[0]), static_cast<uint32_t>(q[1]));
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max(static_cast<uint32_t>(r[0]), static_cast<uint32_t>(r[1]));
+}
+
+// Winner r of a top-k, held by lane r (r < k).
+struct TopK {
+  int e;
+  float val;
+  float aux;
+};
+
+// k largest of v[0..n) (lane-strided registers), ties to the lower index,
+// by k rounds of wave argmax.  Lane r < k returns winner r (index, value,
+// aux[] of the winner); R.sel / R.sval / R.saux get the same lists.  All 64
+// lanes call it.
 template <int P>
-__device__ __forceinline__ void reg_topk(const float (&v)[P], const float (&aux)[P], int n, int k, ZMOE_LDS RouteLds& R) {
+__device__ __forceinline__ TopK reg_topk(const float (&v)[P], const float (&aux)[P], int n, int k, ZMOE_LDS RouteLds& R,
+                                         bool want_aux = false) {
   const int lane = __lane_id();
   uint32_t key[P];
-#pragma unroll
-  for (int i = 0; i < P; ++i) key[i] = (lane + 64 * i < n) ? order_key(v[i]) : 0u;
-  uint32_t T = 0;  // largest threshold with |{key >= T}| >= k
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t cand = T | (1u << bit);
-    int cnt = 0;
-#pragma unroll
-    for (int i = 0; i < P; ++i) cnt += __popcll(__ballot(key[i] >= cand));
-    if (cnt >= k) T = cand;
-  }
-  int need = k;
-#pragma unroll
-  for (int i = 0; i < P; ++i) need -= __popcll(__ballot(key[i] > T));
-  if (lane == 0) R.cnt = 0;
-  wave_lds_sync();
+  bool bf = true;  // every value bf16-representable (low 16 bits zero)
 #pragma unroll
   for (int i = 0; i < P; ++i) {
-    const bool tie = key[i] == T && key[i] != 0u;
-    const uint64_t tm = __ballot(tie);
-    const bool take = key[i] > T || (tie && __popcll(tm & lanes_below_mask(lane)) < need);
-    need -= min(need, __popcll(tm));
-    if (take) {
-      const int pos = __hip_atomic_fetch_add(&R.cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
-      R.wkey[pos] = key[i];
-      R.widx[pos] = lane + 64 * i;
-      R.wval[pos] = v[i];
-      R.waux[pos] = aux[i];
+    key[i] = (lane + 64 * i < n) ? order_key(v[i]) : 0u;
+    bf = bf && ((lane + 64 * i >= n) || (__float_as_uint(v[i]) & 0xFFFFu) == 0u);
+  }
+  TopK mine{0, 0.0f, 0.0f};
+  if (__all(bf) && n <= 0xFFFF) {
+    // bf16 values: (16-bit order key << 16) | (0xFFFF - index) is unique and
+    // orders like (value desc, index asc), so one max finds the winner and
+    // its value decodes from the key.
+    uint32_t pk[P];
+#pragma unroll
+    for (int i = 0; i < P; ++i)
+      pk[i] = (lane + 64 * i < n) ? ((key[i] & 0xFFFF0000u) | (0xFFFFu - static_cast<uint32_t>(lane + 64 * i))) : 0u;
+    uint32_t mine_m = 0;
+    for (int r = 0; r < k; ++r) {
+      uint32_t m = pk[0];
+#pragma unroll
+      for (int i = 1; i < P; ++i) m = max(m, pk[i]);
+      m = wave_max_u32(m);
+#pragma unroll
+      for (int i = 0; i < P; ++i) pk[i] = (pk[i] == m) ? 0u : pk[i];
+      mine_m = (lane == r) ? m : mine_m;
+      if (want_aux) {
+        const int e = __builtin_amdgcn_readfirstlane(static_cast<int>(0xFFFFu - (m & 0xFFFFu)));  // uniform
+        const int wl = e & 63, wi = e >> 6;
+        float wa = 0.0f;
+#pragma unroll
+        for (int i = 0; i < P; ++i)
+          if (i == wi) wa = readlane_f(aux[i], wl);
+        if (lane == r) mine.aux = wa;
+      }
+    }
+    {
+      const uint32_t ok = mine_m >> 16;
+      const uint32_t u16 = (ok & 0x8000u) ? (ok & 0x7FFFu) : (~ok & 0xFFFFu);
+      mine.e = static_cast<int>(0xFFFFu - (mine_m & 0xFFFFu));
+      mine.val = __uint_as_float(u16 << 16);
+    }
+    if (lane < k) {
+      R.sel[lane] = mine.e;
+      R.sval[lane] = mine.val;
+      R.saux[lane] = mine.aux;
+    }
+    wave_lds_sync();
+    return mine;
+  }
+  for (int r = 0; r < k; ++r) {
+    uint32_t m = key[0];
+#pragma unroll
+    for (int i = 1; i < P; ++i) m = max(m, key[i]);
+    m = wave_max_u32(m);
+    // lowest expert index holding the maximum: lowest slot, then lowest lane
+    int wi = 0;
+    uint64_t hit = 0;
+#pragma unroll
+    for (int i = P - 1; i >= 0; --i) {
+      const uint64_t b = __ballot(key[i] == m);
+      if (b) {
+        hit = b;
+        wi = i;
+      }
+    }
+    const int wl = __ffsll(static_cast<unsigned long long>(hit)) - 1;
+    float wv = 0.0f, wa = 0.0f;
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      if (i == wi) {
+        wv = readlane_f(v[i], wl);
+        wa = readlane_f(aux[i], wl);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < P; ++i)
+      if (i == wi && lane == wl) key[i] = 0u;
+    if (lane == r) {
+      mine.e = wl + 64 * wi;
+      mine.val = wv;
+      mine.aux = wa;
     }
   }
-  wave_lds_sync();
   if (lane < k) {
-    const uint32_t kr = R.wkey[lane];
-    const int er = R.widx[lane];
-    int rank = 0;
-    for (int j = 0; j < k; ++j) {
-      const uint32_t kj = R.wkey[j];
-      const int ej = R.widx[j];
-      rank += (kj > kr || (kj == kr && ej < er)) ? 1 : 0;
-    }
-    R.sel[rank] = er;
-    R.sval[rank] = R.wval[lane];
-    R.saux[rank] = R.waux[lane];
+    R.sel[lane] = mine.e;
+    R.sval[lane] = mine.val;
+    R.saux[lane] = mine.aux;
   }
   wave_lds_sync();
+  return mine;
+}
+
+// ((0 + x[lane 0]) + x[lane 1]) + ... + x[lane k-1]: a sum in selection order
+// of per-lane winner values (uniform result).
+__device__ __forceinline__ float ordered_lane_sum(float x, int k) {
+  float s = 0.0f;
+  for (int r = 0; r < k; ++r) s += readlane_f(x, r);
+  return s;
 }
 
 // a/b rounded once to bf16 (the fp32 quotient is corrected when it lands
@@ -173,19 +246,17 @@ __device__ __forceinline__ void route_row(const RouteArgs a, RowVals<P> row, ZMO
     const float s = reg_row_sum(v, E);
 #pragma unroll
     for (int i = 0; i < P; ++i) v[i] = div_to_bf16(v[i], s);
-    reg_topk(v, aux, E, k, R);
-    float tot = 0.0f;
-    for (int r = 0; r < k; ++r) tot += R.sval[r];
-    const float sb = round_bf16(tot);
-    if (lane < k) R.w[lane] = a.norm ? div_to_bf16(R.sval[lane], sb) : R.sval[lane];
+    const TopK t = reg_topk(v, aux, E, k, R);
+    const float sb = round_bf16(ordered_lane_sum(t.val, k));
+    if (lane < k) R.w[lane] = a.norm ? div_to_bf16(t.val, sb) : t.val;
   } else if (a.kind == kRouteTopkLogits) {
     // moe.topk_gating_softmax (moe.py:1239-1396), f32 compute
     if (a.bias == nullptr && a.norm) {
-      reg_topk(v, aux, E, k, R);
-      const float m = R.sval[0];
-      float s = 0.0f;
-      for (int r = 0; r < k; ++r) s += expf(R.sval[r] - m);
-      if (lane < k) R.w[lane] = expf(R.sval[lane] - m) / s;
+      const TopK t = reg_topk(v, aux, E, k, R);
+      const float m = readlane_f(t.val, 0);
+      const float ex = expf(t.val - m);
+      const float s = ordered_lane_sum(ex, k);
+      if (lane < k) R.w[lane] = ex / s;
     } else {
       const float m = reg_row_max(v, E);
 #pragma unroll
@@ -196,10 +267,9 @@ __device__ __forceinline__ void route_row(const RouteArgs a, RowVals<P> row, ZMO
         const int e = lane + 64 * i;
         v[i] = v[i] / s + ((a.bias && e < E) ? gload(a.bias + e) : 0.0f);
       }
-      reg_topk(v, aux, E, k, R);
-      float t = 0.0f;
-      for (int r = 0; r < k; ++r) t += R.sval[r];
-      if (lane < k) R.w[lane] = a.norm ? R.sval[lane] / (t + 1e-20f) : R.sval[lane];
+      const TopK t = reg_topk(v, aux, E, k, R);
+      const float tot = ordered_lane_sum(t.val, k);
+      if (lane < k) R.w[lane] = a.norm ? t.val / (tot + 1e-20f) : t.val;
     }
     if (a.w_bf16 && lane < k) R.w[lane] = round_bf16(R.w[lane]);
   } else {
@@ -234,27 +304,24 @@ __device__ __forceinline__ void route_row(const RouteArgs a, RowVals<P> row, ZMO
       }
       wave_lds_sync();
       // keep the topk_group best groups (ties -> lower group index)
-      const uint32_t gk = lane < ng ? order_key(R.gsc[lane]) : 0u;
-      uint32_t T = 0;
-      for (int bit = 31; bit >= 0; --bit) {
-        const uint32_t cand = T | (1u << bit);
-        if (__popcll(__ballot(gk >= cand)) >= kg) T = cand;
+      uint32_t gk = lane < ng ? order_key(R.gsc[lane]) : 0u;
+      uint64_t keepm = 0;
+      for (int r = 0; r < kg; ++r) {
+        const uint32_t m = wave_max_u32(gk);
+        const int wl = __ffsll(static_cast<unsigned long long>(__ballot(gk == m))) - 1;
+        keepm |= 1ull << wl;
+        if (lane == wl) gk = 0u;
       }
-      const int need = kg - __popcll(__ballot(gk > T));
-      const uint64_t tm = __ballot(gk == T && gk != 0u);
-      const bool keep = gk > T || (gk == T && gk != 0u && __popcll(tm & lanes_below_mask(lane)) < need);
-      const uint64_t keepm = __ballot(keep);
 #pragma unroll
       for (int i = 0; i < P; ++i) {
         const int e = lane + 64 * i;
         if (e < E && !((keepm >> (e / gsz)) & 1ull)) v[i] = 0.0f;
       }
     }
-    reg_topk(v, aux, E, k, R);
-    float s = 0.0f;
-    for (int r = 0; r < k; ++r) s += R.saux[r];
+    const TopK t = reg_topk(v, aux, E, k, R, true);
+    const float s = ordered_lane_sum(t.aux, k);
     if (lane < k) {
-      float x = R.saux[lane] / s;
+      float x = t.aux / s;
       if (a.scale != 1.0f) x = x * a.scale;
       R.w[lane] = x;
     }
