@@ -351,39 +351,58 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
       if (p.out_w) gstore(p.out_w + b * p.K + lane, L.route[b].w[lane]);
     }
   }
-  for (int e = threadIdx.x; e < E; e += blockDim.x) L.slot_of[e] = -1;
-  __syncthreads();
   const int K = p.K;
   const int npairs = B * K;
-  if (threadIdx.x < npairs) L.slot_of[L.route[threadIdx.x / K].sel[threadIdx.x % K]] = 0;
-  __syncthreads();
-  if (wave == 0) {  // unit slots in expert order
-    int base = 0;
-    for (int e0 = 0; e0 < E; e0 += kWave) {
-      const int e = e0 + lane;
-      const bool f = e < E && L.slot_of[e] == 0;
-      const uint64_t m = __ballot(f);
-      if (f) {
-        const int pos = base + __popcll(m & lanes_below_mask(lane));
-        L.slot_of[e] = pos;
-        L.ulist[pos] = e;
-        L.ucount[pos] = 0;
+  if (B == 1) {
+    // one token: unit r is the r-th selected expert (each expert once)
+    if (wave == 0) {
+      if (lane < K) {
+        L.ulist[lane] = L.route[0].sel[lane];
+        L.ucount[lane] = 1;
+        L.upairs[lane][0] = lane;
       }
-      base += __popcll(m);
+      if (lane == 0) {
+        L.nunits = K;
+        if (has_shared) {
+          L.ucount[K] = 1;
+          L.upairs[K][0] = K;
+        }
+      }
     }
-    if (lane == 0) {
-      L.nunits = base;
-      if (has_shared) L.ucount[base] = B;
+    __syncthreads();
+  } else {
+    for (int e = threadIdx.x; e < E; e += blockDim.x) L.slot_of[e] = -1;
+    __syncthreads();
+    if (threadIdx.x < npairs) L.slot_of[L.route[threadIdx.x / K].sel[threadIdx.x % K]] = 0;
+    __syncthreads();
+    if (wave == 0) {  // unit slots in expert order
+      int base = 0;
+      for (int e0 = 0; e0 < E; e0 += kWave) {
+        const int e = e0 + lane;
+        const bool f = e < E && L.slot_of[e] == 0;
+        const uint64_t m = __ballot(f);
+        if (f) {
+          const int pos = base + __popcll(m & lanes_below_mask(lane));
+          L.slot_of[e] = pos;
+          L.ulist[pos] = e;
+          L.ucount[pos] = 0;
+        }
+        base += __popcll(m);
+      }
+      if (lane == 0) {
+        L.nunits = base;
+        if (has_shared) L.ucount[base] = B;
+      }
     }
+    __syncthreads();
+    if (threadIdx.x < npairs) {
+      const int q = threadIdx.x;
+      const int u = L.slot_of[L.route[q / K].sel[q % K]];
+      L.upairs[u][atomicAdd(&L.ucount[u], 1)] = q;
+    }
+    if (has_shared && threadIdx.x < B) L.upairs[L.nunits][threadIdx.x] = npairs + threadIdx.x;
+    __syncthreads();
   }
-  __syncthreads();
-  if (threadIdx.x < npairs) {
-    const int q = threadIdx.x;
-    const int u = L.slot_of[L.route[q / K].sel[q % K]];
-    L.upairs[u][atomicAdd(&L.ucount[u], 1)] = q;
-  }
-  if (has_shared && threadIdx.x < B) L.upairs[L.nunits][threadIdx.x] = npairs + threadIdx.x;
-  __syncthreads();
   const int U = L.nunits;
   const int Uall = U + (has_shared ? 1 : 0);
   trace_mark(p, 5);
