@@ -100,6 +100,28 @@ int zmoe_gather_qmm(void* stream, const void* x, int64_t x_batch,
                     int group_size, int bits, int quant_mode, void* out);
 
 /*
+ * Grouped gather + quantized matmul on MFMA: the batched / prefill form of
+ * zmoe_gather_qmm(_swiglu) for M == 1 rows and many pairs.  Replaces
+ * mx.gather_qmm(..., sorted_indices=True) as mlx_lm's SwitchGLU calls it for
+ * more than one token (the sort path noted at moe_mlp.py:540-543; the
+ * reference's fused op is token-gated to M == 1, moe_mlp.py:298, 523-525).
+ *   out[p, :] = bf16(x[lhs[p], :] . deq(w[rhs[p]])^T)                (up_w NULL)
+ *   out[p, :] = bf16(bf16(g*bf16(sigmoid(g))) * u)  with g, u as above (SwiGLU)
+ * x: bf16 [x_batch, K]; out: bf16 [n_pairs, N] in pair order; rhs need not be
+ * sorted (pairs are counting-sorted by expert in the workspace).  The
+ * products are exact as in the GEMV (fp32 accumulation order differs).
+ * workspace: zmoe_grouped_gather_qmm_workspace_size(...) bytes, no zero-fill.
+ * Requirements: N % 32 == 0, K % 128 == 0, E <= 1024; group_size / mode as
+ * zmoe_gather_qmm.
+ */
+size_t zmoe_grouped_gather_qmm_workspace_size(int64_t n_pairs, int x_batch, int E, int K, int group_size);
+int zmoe_grouped_gather_qmm(void* stream, const void* x, int64_t x_batch, const uint32_t* w, const void* scales,
+                            const void* biases, const uint32_t* up_w, const void* up_scales, const void* up_biases,
+                            const uint32_t* lhs_indices, const uint32_t* rhs_indices, int64_t n_pairs, int N, int K,
+                            int E, int group_size, int bits, int quant_mode, void* workspace, size_t workspace_bytes,
+                            void* out);
+
+/*
  * Dense router projection (the gate nn.Linear of the MoE block,
  * moe_mlp.py:218 `gate_fn(x)`; deepseek_router.py:108 `x @ weight.T`).
  * x: bf16 [B, H]; w: bf16 [E, H]; out: bf16 [B, E] (out_dtype ZMOE_DT_BF16)

@@ -103,6 +103,12 @@ _SIGNATURES = {
         [c_void_p, c_void_p, c_i64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_i64,
          c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p],
     ),
+    "zmoe_grouped_gather_qmm_workspace_size": (c_size_t, [c_i64, c_int, c_int, c_int, c_int]),
+    "zmoe_grouped_gather_qmm": (
+        c_int,
+        [c_void_p, c_void_p, c_i64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_i64, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p, c_size_t, c_void_p],
+    ),
     "zmoe_dense_logits": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]),
     "zmoe_router_softmax_topk": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),
     "zmoe_topk_gating_softmax": (

@@ -1,0 +1,39 @@
+// Grouped (per-expert) quantized GEMM on MFMA (grouped.hip): arguments and
+// host launchers shared with the layer composition.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace zmoe {
+
+struct GroupedArgs {
+  const uint16_t* a;     // activation rows (bf16)
+  int64_t lda;           // elements between rows
+  const float* asum;     // affine: [a rows][K/gs] group sums of a (fp32)
+  const int* offsets;    // [E+1] sorted row ranges; nullptr: one expert, rows [0, M)
+  const int* sorted;     // [rows] pair ids in expert order; nullptr: identity
+  const uint32_t* lhs;   // a row = lhs[pair] when set, else pair / a_div
+  int a_div;             //   (a_div > 0), else the sorted row r itself
+  int scatter;           // out row = sorted[r] (pair order), else r
+  int M;
+  const uint32_t* w0;    // [E, N, K/8] (gate, or the only matrix)
+  const void* s0;
+  const void* b0;
+  const uint32_t* w1;    // up (SwiGLU only)
+  const void* s1;
+  const void* b1;
+  int N, K, gs;
+  uint16_t* out;         // bf16 [rows][ldo]
+  int64_t ldo;
+};
+
+// k_grouped_qmm over every expert's sorted rows; SwiGLU of two matrices when
+// swiglu (w1/s1/b1 = up), else one matrix.
+int launch_grouped(hipStream_t st, const GroupedArgs& g, int n_experts, int quant_mode, bool swiglu);
+// offsets[E+1] / sorted[npairs]: the pairs (token, k) in expert order.
+int launch_sort_pairs(hipStream_t st, const uint32_t* idx, int npairs, int E, int* offsets, int* sorted);
+// out[r][g] = fp32 sum of a[r][g*gs .. +gs).
+int launch_row_group_sums(hipStream_t st, const uint16_t* a, int64_t lda, int rows, int K, int gs, float* out);
+
+}  // namespace zmoe

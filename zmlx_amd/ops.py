@@ -34,6 +34,7 @@ from . import _native as N
 __all__ = [
     "gather_qmm_swiglu",
     "gather_qmm",
+    "gather_qmm_grouped",
     "dense_logits",
     "qwen_gating",
     "topk_gating_softmax",
@@ -226,6 +227,66 @@ def gather_qmm(
     rc = N.lib().zmoe_gather_qmm(
         _stream(dev), _ptr(xc), nx, _ptr(w.contiguous()), _ptr(s), _ptr(b), _ptr(lhs), _ptr(rhs), lhs.numel(),
         M, Nn, K, ne, group_size, bits, qm, _ptr(out),
+    )
+    N.check(rc, op)
+    return out
+
+
+def gather_qmm_grouped(
+    x: torch.Tensor,
+    w: torch.Tensor,
+    scales: torch.Tensor,
+    biases: torch.Tensor | None,
+    lhs_indices: torch.Tensor,
+    rhs_indices: torch.Tensor,
+    *,
+    up: tuple | None = None,
+    group_size: int = 64,
+    bits: int = 4,
+    mode: str = "affine",
+) -> torch.Tensor:
+    """Grouped (expert-sorted) gather + quantized matmul on MFMA for many
+    single-row pairs: ``out[p] = x[lhs[p]] @ deq(w[rhs[p]]).T`` -- or, with
+    ``up=(up_w, up_scales, up_biases)``, the SwiGLU of the two -- in pair
+    order.  x ``(x_batch, K)`` bf16; returns ``(P, N)`` bf16.  The batched
+    counterpart of :func:`gather_qmm` / :func:`gather_qmm_swiglu`
+    (``mx.gather_qmm(..., sorted_indices=True)`` in mlx_lm's prefill)."""
+    op = "gather_qmm"
+    uw, us, ub = up if up is not None else (None, None, None)
+    dev = _require_gpu(op, x, w, scales, biases, lhs_indices, rhs_indices, uw, us, ub)
+    qm = _mode_id(mode)
+    if x.dim() != 2:
+        raise ValueError(f"[{op}] grouped path expects x of shape (x_batch, K).")
+    if w.dim() != 3:
+        raise ValueError(f"[{op}] weights must have shape (E, N, K_packed).")
+    E, Nn = int(w.shape[0]), int(w.shape[1])
+    K = int(x.shape[-1])
+    if int(w.shape[-1]) * (32 // bits) != K:
+        raise ValueError(f"[{op}] weight inner dimension {int(w.shape[-1]) * (32 // bits)} does not match x ({K}).")
+    if up is not None and (uw.shape != w.shape or us.shape != scales.shape):
+        raise ValueError(f"[{op}] gate and up weights must have matching shapes.")
+    lhs = lhs_indices.reshape(-1).to(torch.int32).contiguous()
+    rhs = rhs_indices.reshape(-1).to(torch.int32).contiguous()
+    if lhs.numel() != rhs.numel():
+        raise ValueError(f"[{op}] lhs_indices and rhs_indices must have the same number of elements.")
+    P = int(rhs.numel())
+    xc = _u16(x, op, "x").contiguous()
+    s, b = _c(scales), _c(biases)
+    us_, ub_ = _c(us), _c(ub)
+    if qm == N.Q_AFFINE:
+        if b is None or (up is not None and ub is None):
+            raise ValueError(f"[{op}] affine mode requires biases.")
+        s, b = _u16(s, op, "scales"), _u16(b, op, "biases")
+        if up is not None:
+            us_, ub_ = _u16(us_, op, "scales"), _u16(ub_, op, "biases")
+    L = N.lib()
+    ws_bytes = int(L.zmoe_grouped_gather_qmm_workspace_size(P, int(x.shape[0]), E, K, group_size))
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    out = torch.empty((P, Nn), dtype=torch.bfloat16, device=dev)
+    rc = L.zmoe_grouped_gather_qmm(
+        _stream(dev), _ptr(xc), int(x.shape[0]), _ptr(w.contiguous()), _ptr(s), _ptr(b),
+        _ptr(None if uw is None else uw.contiguous()), _ptr(us_), _ptr(ub_), _ptr(lhs), _ptr(rhs), P, Nn, K, E,
+        group_size, bits, qm, _ptr(ws), ws.numel(), _ptr(out),
     )
     N.check(rc, op)
     return out
