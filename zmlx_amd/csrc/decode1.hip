@@ -1,0 +1,497 @@
+// One-token MoE decode layer in a single launch (B = 1; the path of
+// zmoe_moe_layer for single-token decode, moe_mlp.py:787-1072 patched_call).
+//
+// Same phases, workspace, tagged cross-workgroup exchange and arithmetic as
+// the small-batch kernel of layer_fused.hip (results are bit-identical to it
+// and to the kernel sequence), specialised for one token so that little code
+// sits on the critical path:
+//
+//   R  router partial dots, spread over every workgroup (unit u -> workgroup
+//      u % G, wave u / G) so that each one's weight load is the only HBM
+//      latency before the exchange; x is staged in LDS meanwhile.
+//   T  wave 0 of every workgroup polls the tagged partials, routes, and writes
+//      a per-unit pointer table (gate/up/down weights, scales, biases of each
+//      selected expert and of the shared expert) to LDS.
+//   A  gate/up + SwiGLU: every wave owns a contiguous range of (unit, row)
+//      pairs; the whole range's loads are issued at once, followed at once by
+//      the wave's down-projection loads, so all the layer's weight bytes are in
+//      flight right after routing.  act rows go to the workspace, tagged.
+//   D  every workgroup stages the act rows in LDS (polling their tags); each
+//      wave owns output rows h of every unit, whose weights are already in its
+//      registers, and finishes them with the k-ordered combine and the
+//      shared-expert add without a workgroup barrier.
+//
+// The unit table keeps per-item address arithmetic to one 64-bit add and
+// keeps the kernel within the scalar register file (no spills).
+#include "zmoe_fused.h"
+
+namespace zmoe {
+
+constexpr int kD1MaxUnits = kMaxTopK + 1;
+constexpr int kD1A = 4;  // gate/up items per batch
+constexpr int kD1D = 4;  // down items per batch
+// arrival counters of the act exchange, in the workspace block at p.aflag:
+// kD1Ctrs counters kD1CtrStride words apart, then one launch count per
+// workgroup at word kD1CtrEpoch
+constexpr int kD1Ctrs = 32;
+constexpr int kD1CtrStride = 32;
+constexpr int kD1CtrEpoch = kD1Ctrs * kD1CtrStride;
+
+struct D1Lds {
+  RouteLds route;
+  const uint32_t* w[3][kD1MaxUnits];  // matrix (gate, up, down) x unit
+  const void* s[3][kD1MaxUnits];
+  const void* b[3][kD1MaxUnits];
+};
+
+struct D1Layout {
+  size_t xs, sx, as, asx, ybuf, grow, total;
+};
+
+__host__ __device__ inline D1Layout d1_layout(int H, int I, int E, int Uall, int rpw) {
+  D1Layout o;
+  const int S_H = H / 32, S_I = I / 32;
+  size_t off = (sizeof(D1Lds) + 15) & ~static_cast<size_t>(15);
+  o.xs = off;
+  off += static_cast<size_t>(lds_row_words(S_H)) * 4;
+  o.sx = off;
+  off += static_cast<size_t>(S_H) * 4;
+  off = (off + 15) & ~static_cast<size_t>(15);
+  o.as = off;
+  off += static_cast<size_t>(Uall) * lds_row_words(S_I) * 4;
+  o.asx = off;
+  off += static_cast<size_t>(Uall) * S_I * 4;
+  o.ybuf = off;
+  off += static_cast<size_t>(kFWaves) * rpw * Uall * 4;
+  o.grow = off;
+  off += static_cast<size_t>(E) * 4;
+  o.total = off;
+  return o;
+}
+
+template <int QMODE, int P, bool XR>
+__global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  D1Lds& L = *reinterpret_cast<D1Lds*>(smem);
+
+  const int wave = threadIdx.x / kWave;
+  const int lane = __lane_id();
+  const int G = gridDim.x;
+  const int W = G * kFWaves;
+  const int gw = blockIdx.x * kFWaves + wave;
+  const int E = p.E, K = p.K, H = p.H, I = p.I;
+  const int NC = H >> 9;
+  const int S_H = H >> 5, S_I = I >> 5;
+  const AffineK ak = affine_k();
+  const bool has_shared = p.Is > 0;
+  const int Uall = K + (has_shared ? 1 : 0);
+  const int rpw = (H + W - 1) / W;
+  const D1Layout lay = d1_layout(H, I, E, Uall, rpw);
+  uint32_t* xs = reinterpret_cast<uint32_t*>(smem + lay.xs);
+  float* sx = reinterpret_cast<float*>(smem + lay.sx);
+  uint32_t* as = reinterpret_cast<uint32_t*>(smem + lay.as);
+  float* asx = reinterpret_cast<float*>(smem + lay.asx);
+  float* ybuf = reinterpret_cast<float*>(smem + lay.ybuf);
+  float* grow = reinterpret_cast<float*>(smem + lay.grow);
+
+  trace_mark(p, 0);
+  const unsigned epoch = dev_load(p.sync + kEpochWord + blockIdx.x);
+  const unsigned tag = epoch + 1u;
+  const unsigned tag16 = tag & 0xFFFFu;
+  // launches of this kernel this workgroup completed (arrival-counter target)
+  const unsigned ctag = dev_load(p.aflag + kD1CtrEpoch + blockIdx.x) + 1u;
+
+  // ---------------- R: router partials ----------------
+  for (int u = wave * G + blockIdx.x; u < E * NC; u += W) {
+    const int e = u / NC, c = u - e * NC;
+    const uint4 wv = gload(reinterpret_cast<const uint4*>(p.wr + static_cast<int64_t>(e) * H + c * 512 + lane * 8));
+    const uint4 xv = gload(reinterpret_cast<const uint4*>(p.x + c * 512 + lane * 8));
+    float a = 0.0f;
+    a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv.x), __builtin_bit_cast(bf16x2_t, xv.x), a, false);
+    a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv.y), __builtin_bit_cast(bf16x2_t, xv.y), a, false);
+    a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv.z), __builtin_bit_cast(bf16x2_t, xv.z), a, false);
+    a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv.w), __builtin_bit_cast(bf16x2_t, xv.w), a, false);
+    a = wave_sum(a);
+    if (lane == 0)
+      dev_store(p.rpart + static_cast<int64_t>(e) * NC + c, (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(a));
+  }
+  stage_rows_lds<QMODE, false>(p, p.x, H, 1, S_H, xs, sx, 0u);
+  trace_mark(p, 1);
+  lds_barrier();
+  trace_mark(p, 2);
+
+  // ---------------- T: routing and the unit table ----------------
+  if (wave == 0) {
+    const RowVals<P> row = poll_logits<P>(p, p.rpart, NC, tag);
+    trace_mark(p, 3);
+    route_row<P>(p.route, row, *(ZMOE_LDS RouteLds*)(&L.route), (ZMOE_LDS float*)grow);
+    trace_mark(p, 4);
+    if (blockIdx.x == 0 && lane < K) {
+      if (p.out_idx) gstore(p.out_idx + lane, static_cast<uint32_t>(L.route.sel[lane]));
+      if (p.out_w) gstore(p.out_w + lane, L.route.w[lane]);
+    }
+    if (lane < Uall * 3) {
+      const int u = lane / 3, m = lane - u * 3;
+      if (u < K) {
+        const int64_t e = L.route.sel[u];
+        const int64_t N = (m == 2) ? H : I;
+        const int64_t Kin = (m == 2) ? I : H;
+        const int64_t ppr = (QMODE == ZMOE_Q_AFFINE) ? ((Kin >> 5) >> p.gshift) : (Kin >> 5);
+        const int64_t pb = (QMODE == ZMOE_Q_AFFINE) ? 2 : 1;
+        L.w[m][u] = p.w[m] + e * N * (Kin >> 3);
+        L.s[m][u] = static_cast<const char*>(p.s[m]) + e * N * ppr * pb;
+        L.b[m][u] = (QMODE == ZMOE_Q_AFFINE) ? static_cast<const void*>(static_cast<const char*>(p.b[m]) + e * N * ppr * 2)
+                                             : nullptr;
+      } else {
+        L.w[m][u] = p.w[3 + m];
+        L.s[m][u] = p.s[3 + m];
+        L.b[m][u] = p.b[3 + m];
+      }
+    }
+  }
+  lds_barrier();
+  trace_mark(p, 5);
+
+  // ---------------- D setup: this wave's down-projection loads ----------------
+  // Output rows [h0, h0 + nrows); slot = (row, unit), unit fastest; RPID
+  // slots per load instruction (lane group rsD), TD segments per lane.
+  const int LI = p.LI, RPID = kWave / LI;
+  const int rsD = lane / LI, liD = lane & (LI - 1);
+  const int TD = S_I / LI;
+  const int h0 = gw * rpw;
+  const int nrows = max(0, min(H, h0 + rpw) - h0);
+  const int slots = nrows * Uall;
+  const int n_itemsD = ((slots + RPID - 1) / RPID) * TD;
+  const int64_t wprD = I >> 3;
+  const int64_t pprD = (QMODE == ZMOE_Q_AFFINE) ? (S_I >> p.gshift) : S_I;
+  int d_hl = rsD / Uall, d_u = rsD - (rsD / Uall) * Uall, d_t = 0, d_g = 0;
+  uint4 wd[kD1D];
+  RawParam rd[kD1D];
+  int jhl[kD1D], ju[kD1D], jt[kD1D];
+  bool jvalid[kD1D];
+  // Loads are unconditional so that waits count them: items past the end
+  // repeat the previous item's address (a cache hit), or read x if the wave
+  // has no down work.
+  auto load_down = [&](int base) {
+    const uint32_t* wp = reinterpret_cast<const uint32_t*>(p.x);
+    const void* sp = p.x;
+    const void* bp = p.x;
+    int64_t poff = 0;
+#pragma unroll
+    for (int j = 0; j < kD1D; ++j) {
+      jhl[j] = min(d_hl, max(nrows - 1, 0));
+      ju[j] = d_u;
+      jt[j] = d_t;
+      jvalid[j] = d_g * RPID + rsD < slots;
+      if (base + j < n_itemsD) {
+        const int s = d_t * LI + liD;
+        const int64_t row = h0 + jhl[j];
+        wp = L.w[2][d_u] + row * wprD + s * 4;
+        sp = L.s[2][d_u];
+        bp = L.b[2][d_u];
+        poff = row * pprD + ((QMODE == ZMOE_Q_AFFINE) ? (s >> p.gshift) : s);
+        if (++d_t == TD) {
+          d_t = 0;
+          ++d_g;
+          d_u += RPID;
+          while (d_u >= Uall) {
+            d_u -= Uall;
+            ++d_hl;
+          }
+          d_u = (d_hl >= nrows) ? 0 : d_u;
+        }
+      }
+      wd[j] = gload(reinterpret_cast<const uint4*>(wp));
+      rd[j] = seg_param_load<QMODE>(sp, bp, poff);
+    }
+  };
+
+  // ---------------- A: gate/up + SwiGLU ----------------
+  const int64_t wpr = H >> 3;
+  const int64_t ppr = (QMODE == ZMOE_Q_AFFINE) ? (S_H >> p.gshift) : S_H;
+  if constexpr (XR) {
+    // H = 2048: lane l owns x segment l of the row (registers), one segment
+    // per lane, one wave-wide load per row.
+    const int RA = Uall * I;
+    const int per = (RA + W - 1) / W;
+    const int g0 = min(RA, gw * per), g1 = min(RA, g0 + per);
+    const uint4 x0 = *reinterpret_cast<const uint4*>(xs + ((0 * S_H) + lane) * 4);
+    const uint4 x1 = *reinterpret_cast<const uint4*>(xs + ((1 * S_H) + lane) * 4);
+    const uint4 x2 = *reinterpret_cast<const uint4*>(xs + ((2 * S_H) + lane) * 4);
+    const uint4 x3 = *reinterpret_cast<const uint4*>(xs + ((3 * S_H) + lane) * 4);
+    const float xsum = (QMODE == ZMOE_Q_AFFINE) ? sx[lane] : 0.0f;
+    const int pi = (QMODE == ZMOE_Q_AFFINE) ? (lane >> p.gshift) : lane;
+    int cu = g0 / I;
+    int cr = g0 - cu * I;
+    uint4 wg[kD1A], wu[kD1A];
+    RawParam rg[kD1A], ru[kD1A];
+    int jrow[kD1A], junit[kD1A];
+    auto load_a = [&](int base) {
+      const uint32_t *gwp = nullptr, *uwp = nullptr;
+      const void *gsp = nullptr, *gbp = nullptr, *usp = nullptr, *ubp = nullptr;
+      int64_t poff = 0;
+#pragma unroll
+      for (int j = 0; j < kD1A; ++j) {
+        if (j == 0 || base + j < g1) {
+          gwp = L.w[0][cu] + cr * wpr + lane * 4;
+          uwp = L.w[1][cu] + cr * wpr + lane * 4;
+          gsp = L.s[0][cu];
+          gbp = L.b[0][cu];
+          usp = L.s[1][cu];
+          ubp = L.b[1][cu];
+          poff = cr * ppr + pi;
+          jrow[j] = cr;
+          junit[j] = cu;
+          if (++cr == I) {
+            cr = 0;
+            ++cu;
+          }
+        } else {
+          jrow[j] = jrow[j - 1];
+          junit[j] = junit[j - 1];
+        }
+        wg[j] = gload(reinterpret_cast<const uint4*>(gwp));
+        wu[j] = gload(reinterpret_cast<const uint4*>(uwp));
+        rg[j] = seg_param_load<QMODE>(gsp, gbp, poff);
+        ru[j] = seg_param_load<QMODE>(usp, ubp, poff);
+      }
+    };
+    // down loads first: they stream while the gate/up loads follow, and the
+    // wave's loads all return before the act rows are computed
+    load_down(0);
+    if (g0 < g1) load_a(g0);
+    for (int base = g0; base < g1; base += kD1A) {
+      if (base != g0) load_a(base);
+      float gv[kD1A], uv[kD1A];
+#pragma unroll
+      for (int j = 0; j < kD1A; ++j) {
+        gv[j] = uv[j] = 0.0f;
+        if (j > 0 && base + j >= g1) continue;  // wave-uniform: past the range
+        float sg, cg, su, cu2;
+        seg_param_decode<QMODE>(rg[j], sg, cg);
+        seg_param_decode<QMODE>(ru[j], su, cu2);
+        gv[j] = wave_sum(seg_accum<QMODE>(0.0f, sg, cg, seg_dot<QMODE>(wg[j], x0, x1, x2, x3, ak), xsum));
+        uv[j] = wave_sum(seg_accum<QMODE>(0.0f, su, cu2, seg_dot<QMODE>(wu[j], x0, x1, x2, x3, ak), xsum));
+      }
+      if (base == g0) trace_mark(p, 6);
+      // lane j stores item j (every lane holds every item's sums)
+      float gsel = gv[0], usel = uv[0];
+      int rsel = jrow[0], usel_u = junit[0];
+#pragma unroll
+      for (int j = 1; j < kD1A; ++j) {
+        if (lane == j) {
+          gsel = gv[j];
+          usel = uv[j];
+          rsel = jrow[j];
+          usel_u = junit[j];
+        }
+      }
+      if (lane < kD1A && base + lane < g1)
+        dev_store(p.act + static_cast<int64_t>(usel_u) * p.act_stride + rsel,
+                  (tag16 << 16) | swiglu_bf16(round_bf16(gsel), round_bf16(usel)));
+    }
+  } else {
+    // general H: LH lanes per row (RPI rows per load), T segments per lane,
+    // x from LDS
+    const int LH = p.LH, RPI = kWave / LH;
+    const int rs = lane / LH, li = lane & (LH - 1);
+    const int T = S_H / LH;
+    const int rgu = I / RPI;
+    const int rg_total = Uall * rgu;
+    const int per = (rg_total + W - 1) / W;
+    const int g0 = min(rg_total, gw * per), g1 = min(rg_total, g0 + per);
+    const int n_items = (g1 - g0) * T;
+    int cu = g0 / max(rgu, 1);
+    int crg = g0 - cu * rgu;
+    int ct = 0;
+    uint4 wg[kD1A], wu[kD1A];
+    RawParam rg[kD1A], ru[kD1A];
+    int iu[kD1A], irow[kD1A], it_[kD1A];
+    auto load_a = [&](int base) {
+#pragma unroll
+      for (int j = 0; j < kD1A; ++j) {
+        iu[j] = cu;
+        irow[j] = crg * RPI + rs;
+        it_[j] = ct;
+        if (base + j < n_items) {
+          const int s = ct * LH + li;
+          const int64_t row = irow[j];
+          wg[j] = gload(reinterpret_cast<const uint4*>(L.w[0][cu] + row * wpr + s * 4));
+          wu[j] = gload(reinterpret_cast<const uint4*>(L.w[1][cu] + row * wpr + s * 4));
+          const int pi = (QMODE == ZMOE_Q_AFFINE) ? (s >> p.gshift) : s;
+          rg[j] = seg_param_load<QMODE>(L.s[0][cu], L.b[0][cu], row * ppr + pi);
+          ru[j] = seg_param_load<QMODE>(L.s[1][cu], L.b[1][cu], row * ppr + pi);
+          if (++ct == T) {
+            ct = 0;
+            if (++crg == rgu) {
+              crg = 0;
+              ++cu;
+            }
+          }
+        }
+      }
+    };
+    load_down(0);
+    if (n_items > 0) load_a(0);
+    float ag = 0.0f, au = 0.0f;
+    for (int base = 0; base < n_items; base += kD1A) {
+      if (base > 0) load_a(base);
+#pragma unroll
+      for (int j = 0; j < kD1A; ++j) {
+        if (base + j < n_items) {
+          const int t = it_[j];
+          const int s = t * LH + li;
+          float sgj, cgj, suj, cuj;
+          seg_param_decode<QMODE>(rg[j], sgj, cgj);
+          seg_param_decode<QMODE>(ru[j], suj, cuj);
+          const float xsum = (QMODE == ZMOE_Q_AFFINE) ? sx[s] : 0.0f;
+          ag = seg_accum<QMODE>(t == 0 ? 0.0f : ag, sgj, cgj, seg_dot_lds<QMODE>(wg[j], xs, S_H, 0, s, ak), xsum);
+          au = seg_accum<QMODE>(t == 0 ? 0.0f : au, suj, cuj, seg_dot_lds<QMODE>(wu[j], xs, S_H, 0, s, ak), xsum);
+          if (base == 0 && j == 0) trace_mark(p, 6);
+          if (t == T - 1) {
+            const float gv = lanes_sum(ag, LH);
+            const float uv = lanes_sum(au, LH);
+            if (li == 0)
+              dev_store(p.act + static_cast<int64_t>(iu[j]) * p.act_stride + irow[j],
+                        (tag16 << 16) | swiglu_bf16(round_bf16(gv), round_bf16(uv)));
+          }
+        }
+      }
+    }
+  }
+  trace_mark(p, 7);
+  // All act rows of the grid are stored once every workgroup has arrived:
+  // each wave waits for its own stores (its loads are back already), the
+  // workgroup adds 1 to arrival counter g % 32 (one 128-byte line each), and
+  // wave 0 polls the 32 counters until each holds  launches x its share of
+  // workgroups.  The act read below still verifies every tag.
+  __builtin_amdgcn_s_waitcnt(0);
+  lds_barrier();
+  trace_mark(p, 13);
+  if (threadIdx.x == 0)
+    (void)__hip_atomic_fetch_add((ZMOE_GLOBAL unsigned*)(p.aflag + (blockIdx.x % kD1Ctrs) * kD1CtrStride), 1u,
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (wave == 0) {
+    const int c = lane;
+    const unsigned share = c < kD1Ctrs ? G / kD1Ctrs + (c < G % kD1Ctrs ? 1u : 0u) : 0u;
+    const unsigned target = ctag * share;  // modulo 2^32, compared by difference
+    unsigned spins = 0;
+    for (;;) {
+      const bool ok = c >= kD1Ctrs || static_cast<int>(dev_load(p.aflag + c * kD1CtrStride) - target) >= 0;
+      if (__all(ok)) break;
+      if (++spins > kSpinLimit) {
+        if (lane == 0) wait_timeout(p);
+        break;
+      }
+    }
+    trace_mark(p, 14);
+  }
+  lds_barrier();
+  trace_mark(p, 8);
+
+  // ---------------- D: down projection ----------------
+  stage_rows_lds<QMODE, true>(p, p.act, p.act_stride, Uall, S_I, as, asx, tag16);
+  trace_mark(p, 9);
+  lds_barrier();
+  trace_mark(p, 10);
+  float acc = 0.0f;
+  for (int base = 0; base < n_itemsD; base += kD1D) {
+    if (base > 0) load_down(base);
+#pragma unroll
+    for (int j = 0; j < kD1D; ++j) {
+      if (base + j < n_itemsD) {
+        const int u = ju[j], t = jt[j];
+        const int s = t * LI + liD;
+        float sdj, cdj;
+        seg_param_decode<QMODE>(rd[j], sdj, cdj);
+        const float xsum = (QMODE == ZMOE_Q_AFFINE) ? asx[u * S_I + s] : 0.0f;
+        acc = seg_accum<QMODE>(t == 0 ? 0.0f : acc, sdj, cdj, seg_dot_lds<QMODE>(wd[j], as, S_I, u, s, ak), xsum);
+        if (t == TD - 1) {
+          const float y = lanes_sum(acc, LI);
+          if (liD == 0 && jvalid[j]) ybuf[(wave * rpw + jhl[j]) * Uall + u] = round_bf16(y);
+        }
+      }
+    }
+  }
+  wave_lds_sync();
+  trace_mark(p, 11);
+
+  // ---------------- combine (+ shared expert), per wave ----------------
+  if (lane < nrows) {
+    const float* yr = ybuf + (wave * rpw + lane) * Uall;
+    const float* wk = L.route.w;
+    float o = round_bf16(combine_one(p.combine_mode, K, [&](int k) { return yr[k]; }, [&](int k) { return wk[k]; }));
+    if (has_shared) o = add_nofma(o, yr[K]);
+    gstore(p.out + h0 + lane, static_cast<uint16_t>(f32_to_bf16_bits(o)));
+  }
+  trace_mark(p, 12);
+  if (threadIdx.x == 0) {
+    dev_store(p.sync + kEpochWord + blockIdx.x, epoch + 1);
+    dev_store(p.aflag + kD1CtrEpoch + blockIdx.x, ctag);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+static bool d1_enabled() {
+  static int on = -1;
+  if (on < 0) {
+    const char* e = getenv("ZMOE_DECODE1");
+    on = (e && e[0] == '0') ? 0 : 1;
+  }
+  return on == 1;
+}
+
+size_t decode1_lds_bytes(const zmoe_layer_desc* d, int grid) {
+  const int Uall = d->top_k + (d->shared_inter > 0 ? 1 : 0);
+  const int W = grid * kFWaves;
+  const int rpw = (d->hidden + W - 1) / W;
+  return d1_layout(d->hidden, d->inter, d->n_experts, Uall, rpw).total;
+}
+
+bool decode1_supported(const zmoe_layer_desc* d, int grid) {
+  if (!d1_enabled()) return false;
+  const int LH = gcd_int(d->hidden / 32, kWave);
+  const int LI = gcd_int(d->inter / 32, kWave);
+  if (d->inter % (kWave / LH) != 0) return false;
+  if (d->top_k + 1 > kD1MaxUnits) return false;
+  (void)LI;
+  return decode1_lds_bytes(d, grid) <= 160 * 1024;
+}
+
+template <int QMODE, int P, bool XR>
+static int launch_d1_t(hipStream_t st, const FusedParams& fp, size_t lds, int grid) {
+  static bool prepared = false;
+  const void* fn = reinterpret_cast<const void*>(&k_moe_decode1<QMODE, P, XR>);
+  if (!prepared) {
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    prepared = true;
+  }
+  int occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, kFThreads, lds) != hipSuccess || occ < 1)
+    return fail(ZMOE_EUNSUPPORTED, "[moe_layer] one-token kernel cannot be resident on every CU");
+  hipLaunchKernelGGL((k_moe_decode1<QMODE, P, XR>), dim3(grid), dim3(kFThreads), lds, st, fp);
+  return check_launch("moe_layer(one-token launch)");
+}
+
+template <int QMODE, bool XR>
+static int launch_d1_q(hipStream_t st, const FusedParams& fp, size_t lds, int grid) {
+  switch (route_slots(fp.E)) {
+    case 1: return launch_d1_t<QMODE, 1, XR>(st, fp, lds, grid);
+    case 2: return launch_d1_t<QMODE, 2, XR>(st, fp, lds, grid);
+    case 4: return launch_d1_t<QMODE, 4, XR>(st, fp, lds, grid);
+    case 8: return launch_d1_t<QMODE, 8, XR>(st, fp, lds, grid);
+    default: return launch_d1_t<QMODE, 16, XR>(st, fp, lds, grid);
+  }
+}
+
+int launch_decode1(hipStream_t st, const zmoe_layer_desc* d, const FusedParams& fp, int grid) {
+  const size_t lds = decode1_lds_bytes(d, grid);
+  const bool xr = fp.LH == kWave && fp.H == 32 * kWave;
+  if (d->quant_mode == ZMOE_Q_AFFINE)
+    return xr ? launch_d1_q<ZMOE_Q_AFFINE, true>(st, fp, lds, grid) : launch_d1_q<ZMOE_Q_AFFINE, false>(st, fp, lds, grid);
+  return xr ? launch_d1_q<ZMOE_Q_MXFP4, true>(st, fp, lds, grid) : launch_d1_q<ZMOE_Q_MXFP4, false>(st, fp, lds, grid);
+}
+
+}  // namespace zmoe

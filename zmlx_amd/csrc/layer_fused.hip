@@ -35,229 +35,9 @@
 // register-resident fast path.  The arithmetic is the multi-kernel path's
 // (same dot products, reduction trees, routing code and combine): results
 // are bit-identical to it.
-#include "zmoe_common.h"
-#include "zmoe_combine.h"
-#include "zmoe_host.h"
-#include "zmoe_route.h"
+#include "zmoe_fused.h"
 
 namespace zmoe {
-
-constexpr int kFThreads = 512;
-constexpr int kFWaves = kFThreads / kWave;
-constexpr int kFMaxB = 8;                 // tokens per call on the fused path
-constexpr int kFMaxUnits = kFMaxB * kMaxTopK + 1;
-constexpr int kChunkA = 4;                // (row-group, segment) items per batch, phase A
-constexpr int kChunkD = 4;                // (slot-group, segment) items per batch, phase D
-constexpr unsigned kSpinLimit = 1u << 21;
-constexpr int kTraceSlots = 16;
-// words of the workspace's leading state block
-constexpr int kErrWord = static_cast<int>(kSyncErrorByte / 4);
-constexpr int kEpochWord = 64;  // + workgroup: launches completed
-constexpr int kMaxGrid = static_cast<int>(kSyncBlockBytes / 4) - kEpochWord;
-constexpr int kMaxNC = 16;                // router chunks of 512 (H <= 8192)
-
-struct FusedParams {
-  int H, E, K, I, Is, B;
-  int gshift, combine_mode;
-  RouteArgs route;
-  int LH, LI;            // lanes per row for K_in = H / K_in = I (= Is)
-  const uint16_t* x;
-  uint16_t* out;
-  const uint16_t* wr;
-  const uint32_t* w[6];  // gate, up, down, sh_gate, sh_up, sh_down
-  const void* s[6];
-  const void* b[6];
-  unsigned* sync;        // state block (words kErrWord, kEpochWord + g)
-  unsigned long long* rpart;  // [B][E][NC]: f32 bits | tag << 32
-  uint32_t* act;         // [B*K + B][act_stride]: bf16 bits | (tag & 0xFFFF) << 16
-  int act_stride;
-  uint32_t* out_idx;
-  float* out_w;
-  unsigned long long* trace;  // nullable: [G][kTraceSlots] realtime stamps
-};
-
-struct FusedLds {
-  int ulist[kFMaxUnits];   // expert of each unit (slot order = expert order)
-  int ucount[kFMaxUnits];
-  int upairs[kFMaxUnits][kFMaxB];
-  int nunits;              // routed units; the shared unit (if any) is index nunits
-  int slot_of[1024];
-  RouteLds route[kFMaxB];
-};
-
-__device__ __forceinline__ void trace_mark(const FusedParams& p, int slot) {
-  if (p.trace && threadIdx.x == 0) gstore(p.trace + blockIdx.x * kTraceSlots + slot, static_cast<unsigned long long>(wall_clock64()));
-}
-
-__device__ __forceinline__ void wait_timeout(const FusedParams& p) {
-  __hip_atomic_fetch_or((ZMOE_GLOBAL unsigned*)(p.sync + kErrWord), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Router logits of one token, lane-strided (e = lane + 64 i): the H/512
-// partials of each expert, summed in chunk order once every one of them
-// carries `tag`, rounded to bf16 (the gate Linear returns bf16 logits).
-template <int P>
-__device__ __forceinline__ RowVals<P> poll_logits(const FusedParams& p, const unsigned long long* rp, int NC,
-                                                  unsigned tag) {
-  const int lane = __lane_id();
-  RowVals<P> row;
-  unsigned n = 0;
-  for (;;) {
-    bool ok = true;
-#pragma unroll
-    for (int i = 0; i < P; ++i) {
-      const int e = lane + 64 * i;
-      if (e < p.E) {
-        unsigned long long part[kMaxNC];
-#pragma unroll
-        for (int c = 0; c < kMaxNC; ++c)
-          if (c < NC) part[c] = dev_load(rp + e * NC + c);
-        float a = 0.0f;
-#pragma unroll
-        for (int c = 0; c < kMaxNC; ++c) {
-          if (c < NC) {
-            ok = ok && static_cast<unsigned>(part[c] >> 32) == tag;
-            a += __uint_as_float(static_cast<uint32_t>(part[c]));  // chunks in order
-          }
-        }
-        row.v[i] = round_bf16(a);
-      } else {
-        row.v[i] = -INFINITY;
-      }
-    }
-    if (__all(ok)) break;
-    if (++n > kSpinLimit) {
-      if (lane == 0) wait_timeout(p);
-      break;
-    }
-  }
-  return row;
-}
-
-// bf16 rows -> LDS tile in the layout of qmv.hip (stage_x_row):
-//   xs[((r*4 + j)*S + s)*4 + d], sums sx[r*S + s] (affine).
-// DEV: read the rows with device-coherent 64-bit loads (rows written by
-// other workgroups in this launch).
-template <int QMODE, bool DEV>
-__device__ __forceinline__ void stage_rows_lds(const FusedParams& p, const void* __restrict__ src, int64_t src_stride,
-                                               int nrows, int S, uint32_t* xs, float* sx, unsigned tag16) {
-  // all (row, segment, quarter) items at once, two per thread per round, so
-  // the loads of every row are in flight together
-  const int S4 = S * 4;
-  const int n = nrows * S4;
-  for (int i0 = threadIdx.x; i0 < n; i0 += 2 * kFThreads) {
-    uint4 v[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int i = i0 + h * kFThreads;
-      if (i < n) {
-        const int r = i / S4, rem = i - r * S4;  // segment rem>>2, quarter rem&3
-        if (DEV) {
-          // 8 tagged words (bf16 | tag<<16), polled until all are current
-          const unsigned long long* q =
-              reinterpret_cast<const unsigned long long*>(static_cast<const uint32_t*>(src) + r * src_stride + rem * 8);
-          const unsigned long long want = (static_cast<unsigned long long>(tag16) << 48) | (tag16 << 16);
-          const unsigned long long tmask = 0xFFFF0000FFFF0000ull;
-          unsigned long long w0, w1, w2, w3;
-          unsigned n = 0;
-          for (;;) {
-            w0 = dev_load(q);
-            w1 = dev_load(q + 1);
-            w2 = dev_load(q + 2);
-            w3 = dev_load(q + 3);
-            if (((w0 & tmask) == want) && ((w1 & tmask) == want) && ((w2 & tmask) == want) && ((w3 & tmask) == want))
-              break;
-            if (++n > kSpinLimit) {
-              wait_timeout(p);
-              break;
-            }
-          }
-          auto pair = [](unsigned long long w) {
-            return static_cast<uint32_t>(w & 0xFFFFu) | static_cast<uint32_t>((w >> 16) & 0xFFFF0000u);
-          };
-          v[h] = make_uint4(pair(w0), pair(w1), pair(w2), pair(w3));
-        } else {
-          v[h] = gload(reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(src) + r * src_stride + rem * 8));
-        }
-      }
-    }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int i = i0 + h * kFThreads;
-      if (i < n) {
-        const int r = i / S4, rem = i - r * S4;
-        const int s = rem >> 2, j = rem & 3;
-        uint4 o;
-        if (QMODE == ZMOE_Q_AFFINE) {
-          o.x = (v[h].x & 0xFFFFu) | (v[h].z << 16);
-          o.y = (v[h].x >> 16) | (v[h].z & 0xFFFF0000u);
-          o.z = (v[h].y & 0xFFFFu) | (v[h].w << 16);
-          o.w = (v[h].y >> 16) | (v[h].w & 0xFFFF0000u);
-        } else {
-          o = v[h];
-        }
-        *reinterpret_cast<uint4*>(xs + ((r * 4 + j) * S + s) * 4) = o;
-      }
-    }
-  }
-  if (QMODE == ZMOE_Q_AFFINE) {
-    lds_barrier();
-    for (int i = threadIdx.x; i < nrows * S; i += kFThreads) {
-      const int r = i / S, s = i - r * S;
-      float acc = 0.0f;
-      for (int w = 0; w < 4; ++w) {
-        // pairs (e0,e4) (e1,e5) (e2,e6) (e3,e7) summed in natural order:
-        // (e0+e1) (e2+e3) (e4+e5) (e6+e7), as stage_x_row does
-        const uint4 o = *reinterpret_cast<const uint4*>(xs + ((r * 4 + w) * S + s) * 4);
-        acc += bf16_bits_to_f32(o.x & 0xFFFFu) + bf16_bits_to_f32(o.y & 0xFFFFu);
-        acc += bf16_bits_to_f32(o.z & 0xFFFFu) + bf16_bits_to_f32(o.w & 0xFFFFu);
-        acc += bf16_bits_to_f32(o.x >> 16) + bf16_bits_to_f32(o.y >> 16);
-        acc += bf16_bits_to_f32(o.z >> 16) + bf16_bits_to_f32(o.w >> 16);
-      }
-      sx[r * S + s] = acc;
-    }
-  }
-}
-
-template <int QMODE>
-__device__ __forceinline__ float seg_dot_lds(const uint4 w, const uint32_t* xs, int S, int r, int s, AffineK k) {
-  const uint4 x0 = *reinterpret_cast<const uint4*>(xs + ((r * 4 + 0) * S + s) * 4);
-  const uint4 x1 = *reinterpret_cast<const uint4*>(xs + ((r * 4 + 1) * S + s) * 4);
-  const uint4 x2 = *reinterpret_cast<const uint4*>(xs + ((r * 4 + 2) * S + s) * 4);
-  const uint4 x3 = *reinterpret_cast<const uint4*>(xs + ((r * 4 + 3) * S + s) * 4);
-  return seg_dot<QMODE>(w, x0, x1, x2, x3, k);
-}
-
-// Quantisation parameters of one (row, segment): loaded raw, decoded at use
-// (decoding right after the load would make the load's wait immediate).
-struct RawParam {
-  uint32_t s, b;
-};
-
-template <int QMODE>
-__device__ __forceinline__ RawParam seg_param_load(const void* __restrict__ scales, const void* __restrict__ biases,
-                                                   int64_t idx) {
-  RawParam r;
-  if (QMODE == ZMOE_Q_AFFINE) {
-    r.s = gload(static_cast<const uint16_t*>(scales) + idx);
-    r.b = gload(static_cast<const uint16_t*>(biases) + idx);
-  } else {
-    r.s = gload(static_cast<const uint8_t*>(scales) + idx);
-    r.b = 0;
-  }
-  return r;
-}
-
-template <int QMODE>
-__device__ __forceinline__ void seg_param_decode(RawParam r, float& s, float& c) {
-  if (QMODE == ZMOE_Q_AFFINE) {
-    s = bf16_bits_to_f32(r.s);
-    c = bf16_bits_to_f32(r.b) - 128.0f * s;
-  } else {
-    s = e8m0_to_f32(r.s);
-    c = 0.0f;
-  }
-}
 
 struct UnitPtr {
   const uint32_t* w;
@@ -313,7 +93,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
 
   // phase R..A LDS: x tile, x sums, grouped-router scratch, accumulators
   uint32_t* xs = reinterpret_cast<uint32_t*>(big);
-  float* sx = reinterpret_cast<float*>(xs + static_cast<size_t>(B) * S_H * 16);
+  float* sx = reinterpret_cast<float*>(xs + static_cast<size_t>(B) * lds_row_words(S_H));
   float* rv = sx + static_cast<size_t>(B) * S_H;    // [B][E]
   float* accA = rv + static_cast<size_t>(B) * E;    // [waves][2][B][64]
 
@@ -639,7 +419,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
   const int P0 = npairs;
   const int Ptot = npairs + (has_shared ? B : 0);
   uint32_t* as = reinterpret_cast<uint32_t*>(big);
-  float* asx = reinterpret_cast<float*>(as + static_cast<size_t>(Ptot) * S_I * 16);
+  float* asx = reinterpret_cast<float*>(as + static_cast<size_t>(Ptot) * lds_row_words(S_I));
   float* ybuf = asx + static_cast<size_t>(Ptot) * S_I;                         // [wg rows][Ptot]
   float* accD = ybuf + static_cast<size_t>(kFWaves) * rows_per_wave * Ptot;   // [waves][B][64]
   stage_rows_lds<QMODE, true>(p, p.act, p.act_stride, Ptot, S_I, as, asx, tag16);
@@ -716,9 +496,9 @@ size_t fused_lds_bytes(const zmoe_layer_desc* d, int B) {
   const int Ptot = B * d->top_k + (d->shared_inter > 0 ? B : 0);
   const int G = num_cus();
   const int rows_per_wave = (d->hidden + G * kFWaves - 1) / (G * kFWaves);
-  const size_t front = static_cast<size_t>(B) * S_H * 68 + static_cast<size_t>(B) * d->n_experts * 4 +
+  const size_t front = static_cast<size_t>(B) * (lds_row_words(S_H) * 4 + S_H * 4) + static_cast<size_t>(B) * d->n_experts * 4 +
                        static_cast<size_t>(kFWaves) * 2 * B * kWave * 4;
-  const size_t back = static_cast<size_t>(Ptot) * S_I * 68 + static_cast<size_t>(kFWaves) * rows_per_wave * Ptot * 4 +
+  const size_t back = static_cast<size_t>(Ptot) * (lds_row_words(S_I) * 4 + S_I * 4) + static_cast<size_t>(kFWaves) * rows_per_wave * Ptot * 4 +
                       static_cast<size_t>(kFWaves) * B * kWave * 4;
   return ((sizeof(FusedLds) + 15) & ~static_cast<size_t>(15)) + (front > back ? front : back);
 }
@@ -739,10 +519,13 @@ static size_t off_rpart() { return kSyncBlockBytes; }
 static size_t off_act(const zmoe_layer_desc* d, int B) {
   return align256(off_rpart() + static_cast<size_t>(B) * d->n_experts * (d->hidden / 512) * 8);
 }
-static size_t off_trace(const zmoe_layer_desc* d, int B) {
+static size_t off_flags(const zmoe_layer_desc* d, int B) {
   const int stride = d->inter > d->shared_inter ? d->inter : d->shared_inter;
   const size_t Ptot = static_cast<size_t>(B) * d->top_k + (d->shared_inter > 0 ? B : 0);
   return align256(off_act(d, B) + Ptot * stride * 4);
+}
+static size_t off_trace(const zmoe_layer_desc* d, int B) {
+  return align256(off_flags(d, B) + 4096 + static_cast<size_t>(num_cus()) * 4);
 }
 
 size_t fused_workspace_bytes(const zmoe_layer_desc* d, int B) {
@@ -822,10 +605,12 @@ int launch_fused(hipStream_t st, const zmoe_layer_desc* d, const void* x, int B,
   fp.sync = reinterpret_cast<unsigned*>(base);
   fp.rpart = reinterpret_cast<unsigned long long*>(base + off_rpart());
   fp.act = reinterpret_cast<uint32_t*>(base + off_act(d, B));
+  fp.aflag = reinterpret_cast<unsigned*>(base + off_flags(d, B));
   fp.act_stride = d->inter > d->shared_inter ? d->inter : d->shared_inter;
   fp.out_idx = out_idx;
   fp.out_w = out_w;
   fp.trace = (d->flags & ZMOE_LAYER_TRACE) ? reinterpret_cast<unsigned long long*>(base + off_trace(d, B)) : nullptr;
+  if (B == 1 && decode1_supported(d, num_cus())) return launch_decode1(st, d, fp, num_cus());
   const size_t lds = fused_lds_bytes(d, B);
   if (d->quant_mode == ZMOE_Q_AFFINE) return launch_fused_q<ZMOE_Q_AFFINE>(st, fp, lds);
   return launch_fused_q<ZMOE_Q_MXFP4>(st, fp, lds);
