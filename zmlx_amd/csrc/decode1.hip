@@ -37,8 +37,11 @@ constexpr int kD1Ctrs = 32;
 constexpr int kD1CtrStride = 32;
 constexpr int kD1CtrEpoch = kD1Ctrs * kD1CtrStride;
 
+constexpr int kD1RankMaxE = 256;  // parallel ranking for E <= this
+
 struct D1Lds {
   RouteLds route;
+  uint32_t keys[kD1RankMaxE];         // packed (bf16 order key << 16 | 0xFFFF - e)
   const uint32_t* w[3][kD1MaxUnits];  // matrix (gate, up, down) x unit
   const void* s[3][kD1MaxUnits];
   const void* b[3][kD1MaxUnits];
@@ -69,12 +72,82 @@ __host__ __device__ inline D1Layout d1_layout(int H, int I, int E, int Uall, int
   return o;
 }
 
+// Unit u's pointers for matrix m (0 gate, 1 up, 2 down): routed expert e, or
+// the shared expert for e < 0.
+__device__ __forceinline__ void set_unit_e(const FusedParams& p, D1Lds& L, int u, int m, int e) {
+  if (e >= 0) {
+    L.w[m][u] = p.w[m] + static_cast<int64_t>(e) * p.d1.wst[m];
+    L.s[m][u] = static_cast<const char*>(p.s[m]) + static_cast<int64_t>(e) * p.d1.sst[m];
+    L.b[m][u] = p.b[m] ? static_cast<const void*>(static_cast<const char*>(p.b[m]) + static_cast<int64_t>(e) * p.d1.sst[m])
+                       : nullptr;
+  } else {
+    L.w[m][u] = p.w[3 + m];
+    L.s[m][u] = p.s[3 + m];
+    L.b[m][u] = p.b[3 + m];
+  }
+}
+
+// Rank of key i (number of larger keys; keys are unique) over an EPAD-entry
+// row, Q = 512/EPAD adjacent threads per key, each counting one slice.
+// Returns the rank in thread q == 0 of each group (-1 elsewhere).
+template <int EPAD>
+__device__ __forceinline__ int rank_in_row(const uint32_t* keys, int& i, uint32_t& ki) {
+  constexpr int Q = kFThreads / EPAD;
+  constexpr int PER = EPAD / Q;
+  static_assert(Q >= 2 && Q <= 8 && PER % 4 == 0, "rank slices");
+  i = threadIdx.x / Q;
+  const int q = threadIdx.x % Q;
+  ki = keys[i];
+  uint4 kk[PER / 4];
+#pragma unroll
+  for (int c = 0; c < PER / 4; ++c) kk[c] = *reinterpret_cast<const uint4*>(&keys[q * PER + 4 * c]);
+  int c0 = 0, c1 = 0, c2 = 0, c3 = 0;
+#pragma unroll
+  for (int c = 0; c < PER / 4; ++c) {
+    c0 += kk[c].x > ki ? 1 : 0;
+    c1 += kk[c].y > ki ? 1 : 0;
+    c2 += kk[c].z > ki ? 1 : 0;
+    c3 += kk[c].w > ki ? 1 : 0;
+  }
+  int cnt = (c0 + c1) + (c2 + c3);
+  cnt += __builtin_amdgcn_update_dpp(0, cnt, kDppQuadSwap1, 0xF, 0xF, false);
+  if (Q >= 4) cnt += __builtin_amdgcn_update_dpp(0, cnt, kDppQuadSwap2, 0xF, 0xF, false);
+  if (Q >= 8) cnt += __builtin_amdgcn_update_dpp(0, cnt, kDppHalfMirror, 0xF, 0xF, false);
+  return q == 0 ? cnt : -1;
+}
+
+// Gate weights of the ranked winners (wave 0; lane r < K holds winner r),
+// then the routing outputs of workgroup 0.
+__device__ __forceinline__ void rank_weights(const FusedParams& p, D1Lds& L, int K) {
+  const int lane = __lane_id();
+  const float val = lane < K ? L.route.sval[lane] : 0.0f;
+  float w;
+  if (p.route.kind == kRouteSoftmaxProbs) {
+    const float sb = round_bf16(ordered_lane_sum(val, K));
+    w = p.route.norm ? div_to_bf16(val, sb) : val;
+  } else {
+    // moe.topk_gating_softmax renorm path (moe.py:1239-1396)
+    const float m = readlane_f(val, 0);
+    const float ex = expf(val - m);
+    const float sum = ordered_lane_sum(ex, K);
+    w = ex / sum;
+    if (p.route.w_bf16) w = round_bf16(w);
+  }
+  if (lane < K) {
+    L.route.w[lane] = w;
+    if (blockIdx.x == 0) {
+      if (p.out_idx) gstore(p.out_idx + lane, static_cast<uint32_t>(L.route.sel[lane]));
+      if (p.out_w) gstore(p.out_w + lane, w);
+    }
+  }
+}
+
 template <int QMODE, int P, bool XR>
 __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   D1Lds& L = *reinterpret_cast<D1Lds*>(smem);
 
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
   const int lane = __lane_id();
   const int G = gridDim.x;
   const int W = G * kFWaves;
@@ -84,8 +157,9 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
   const int S_H = H >> 5, S_I = I >> 5;
   const AffineK ak = affine_k();
   const bool has_shared = p.Is > 0;
-  const int Uall = K + (has_shared ? 1 : 0);
-  const int rpw = (H + W - 1) / W;
+  const D1Plan& pl = p.d1;
+  const int Uall = pl.Uall;
+  const int rpw = pl.rpw;
   const D1Layout lay = d1_layout(H, I, E, Uall, rpw);
   uint32_t* xs = reinterpret_cast<uint32_t*>(smem + lay.xs);
   float* sx = reinterpret_cast<float*>(smem + lay.sx);
@@ -101,9 +175,44 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
   // launches of this kernel this workgroup completed (arrival-counter target)
   const unsigned ctag = dev_load(p.aflag + kD1CtrEpoch + blockIdx.x) + 1u;
 
+  // Work assignment (independent of the routing, computed and pinned here so
+  // that none of it runs after the routing wait):
+  // phase D: output rows [h0, h0 + nrows); slot = (row, unit), unit fastest;
+  // RPID slots per load instruction (lane group rsD), TD segments per lane.
+  const int LI = 1 << pl.lLI, RPID = kWave >> pl.lLI;
+  const int rsD = lane >> pl.lLI, liD = lane & (LI - 1);
+  const int TD = pl.TD;
+  int h0 = gw * rpw;
+  int nrows = max(0, min(H, h0 + rpw) - h0);
+  int slots = nrows * Uall;
+  int n_itemsD = ((slots + RPID - 1) >> (6 - pl.lLI)) * TD;
+  int d_hl = static_cast<int>(fdiv(static_cast<uint32_t>(rsD), pl.by_Uall));
+  int d_u = rsD - d_hl * Uall, d_t = 0, d_g = 0;
+  pin_s(h0);
+  pin_s(nrows);
+  pin_s(slots);
+  pin_s(n_itemsD);
+  asm volatile("" : "+v"(d_hl), "+v"(d_u));
+  // phase A: a contiguous range of (unit, row-group) items
+  int a_g0, a_g1, a_cu, a_cr;
+  {
+    const int rg_total = Uall * pl.rgu;
+    a_g0 = min(rg_total, gw * pl.perA);
+    a_g1 = min(rg_total, a_g0 + pl.perA);
+    a_cu = static_cast<int>(fdiv(static_cast<uint32_t>(a_g0), pl.by_rgu));
+    a_cr = a_g0 - a_cu * pl.rgu;
+  }
+  pin_s(a_g0);
+  pin_s(a_g1);
+  pin_s(a_cu);
+  pin_s(a_cr);
+
   // ---------------- R: router partials ----------------
+  // Unit (e, c) = 512-column chunk c of router row e, on workgroup u % G,
+  // wave u / G: the lane's 8-element dot and a wave sum, published as one
+  // tagged word (f32 | tag << 32); readers add the chunks in order.
   for (int u = wave * G + blockIdx.x; u < E * NC; u += W) {
-    const int e = u / NC, c = u - e * NC;
+    const int e = static_cast<int>(fdiv(static_cast<uint32_t>(u), pl.by_NC)), c = u - e * NC;
     const uint4 wv = gload(reinterpret_cast<const uint4*>(p.wr + static_cast<int64_t>(e) * H + c * 512 + lane * 8));
     const uint4 xv = gload(reinterpret_cast<const uint4*>(p.x + c * 512 + lane * 8));
     float a = 0.0f;
@@ -115,56 +224,85 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
     if (lane == 0)
       dev_store(p.rpart + static_cast<int64_t>(e) * NC + c, (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(a));
   }
-  stage_rows_lds<QMODE, false>(p, p.x, H, 1, S_H, xs, sx, 0u);
+  stage_rows_lds<QMODE, false>(p, p.x, H, 1, S_H, xs, sx, 0u, p.by_S4H, p.by_SH);
   trace_mark(p, 1);
   lds_barrier();
   trace_mark(p, 2);
 
   // ---------------- T: routing and the unit table ----------------
+  // Softmax-probability routers (and top-k over logits with renormalised
+  // weights) select by ranking: wave 0 writes one unique key per expert
+  // (bf16 value order, then lower index first), every thread counts the keys
+  // above one expert's key over a slice of the row, and the expert of rank r
+  // becomes winner r -- the same winners in the same order as k rounds of
+  // argmax, with a short dependency chain spread over the workgroup.  The
+  // thread that finds rank r writes unit r's pointers; the gate weights are
+  // only needed by the final combine, so wave 0 computes them later, while
+  // its weight loads are in flight.  Other routers run route_row in wave 0.
+  const int rkind = p.route.kind;
+  const bool rank_route = E <= kD1RankMaxE && K <= kMaxTopK &&
+                          (rkind == kRouteSoftmaxProbs ||
+                           (rkind == kRouteTopkLogits && p.route.bias == nullptr && p.route.norm));
+  const int Epad = E <= 64 ? 64 : (E <= 128 ? 128 : 256);
   if (wave == 0) {
-    const RowVals<P> row = poll_logits<P>(p, p.rpart, NC, tag);
+    RowVals<P> row = poll_logits<P>(p, p.rpart, NC, tag);
     trace_mark(p, 3);
-    route_row<P>(p.route, row, *(ZMOE_LDS RouteLds*)(&L.route), (ZMOE_LDS float*)grow);
-    trace_mark(p, 4);
-    if (blockIdx.x == 0 && lane < K) {
-      if (p.out_idx) gstore(p.out_idx + lane, static_cast<uint32_t>(L.route.sel[lane]));
-      if (p.out_w) gstore(p.out_w + lane, L.route.w[lane]);
-    }
-    if (lane < Uall * 3) {
-      const int u = lane / 3, m = lane - u * 3;
-      if (u < K) {
-        const int64_t e = L.route.sel[u];
-        const int64_t N = (m == 2) ? H : I;
-        const int64_t Kin = (m == 2) ? I : H;
-        const int64_t ppr = (QMODE == ZMOE_Q_AFFINE) ? ((Kin >> 5) >> p.gshift) : (Kin >> 5);
-        const int64_t pb = (QMODE == ZMOE_Q_AFFINE) ? 2 : 1;
-        L.w[m][u] = p.w[m] + e * N * (Kin >> 3);
-        L.s[m][u] = static_cast<const char*>(p.s[m]) + e * N * ppr * pb;
-        L.b[m][u] = (QMODE == ZMOE_Q_AFFINE) ? static_cast<const void*>(static_cast<const char*>(p.b[m]) + e * N * ppr * 2)
-                                             : nullptr;
-      } else {
-        L.w[m][u] = p.w[3 + m];
-        L.s[m][u] = p.s[3 + m];
-        L.b[m][u] = p.b[3 + m];
+    if (rank_route) {
+      float(&v)[P] = row.v;
+      if (rkind == kRouteSoftmaxProbs) {
+        // moe_mlp.py:255-266: precise softmax, probabilities rounded to bf16
+        const float m = reg_row_max(v, E);
+#pragma unroll
+        for (int i = 0; i < P; ++i) v[i] = expf(v[i] - m);
+        const float sum = reg_row_sum(v, E);
+#pragma unroll
+        for (int i = 0; i < P; ++i) v[i] = div_to_bf16(v[i], sum);
+      }
+#pragma unroll
+      for (int i = 0; i < P; ++i) {
+        const int e = lane + 64 * i;
+        if (e < Epad)
+          L.keys[e] = e < E ? ((order_key(v[i]) & 0xFFFF0000u) | (0xFFFFu - static_cast<uint32_t>(e))) : 0u;
+      }
+      trace_mark(p, 15);
+    } else {
+      route_row<P>(p.route, row, *(ZMOE_LDS RouteLds*)(&L.route), (ZMOE_LDS float*)grow);
+      if (lane < Uall * 3) set_unit_e(p, L, lane / 3, lane % 3, lane / 3 < K ? L.route.sel[lane / 3] : -1);
+      if (blockIdx.x == 0 && lane < K) {
+        if (p.out_idx) gstore(p.out_idx + lane, static_cast<uint32_t>(L.route.sel[lane]));
+        if (p.out_w) gstore(p.out_w + lane, L.route.w[lane]);
       }
     }
   }
   lds_barrier();
+  trace_mark(p, 16);
+  if (rank_route) {
+    int i, r;
+    uint32_t ki;
+    if (Epad == 64) r = rank_in_row<64>(L.keys, i, ki);
+    else if (Epad == 128) r = rank_in_row<128>(L.keys, i, ki);
+    else r = rank_in_row<256>(L.keys, i, ki);
+    if (r >= 0 && i < E && r < K) {
+      const uint32_t ok = ki >> 16;
+      const uint32_t u16 = (ok & 0x8000u) ? (ok & 0x7FFFu) : (~ok & 0xFFFFu);
+      L.route.sel[r] = i;
+      L.route.sval[r] = __uint_as_float(u16 << 16);
+#pragma unroll
+      for (int m = 0; m < 3; ++m) set_unit_e(p, L, r, m, i);
+    }
+    if (has_shared && threadIdx.x == kFThreads - 1) {
+#pragma unroll
+      for (int m = 0; m < 3; ++m) set_unit_e(p, L, K, m, -1);
+    }
+    trace_mark(p, 17);
+  }
+  trace_mark(p, 4);
+  lds_barrier();
   trace_mark(p, 5);
 
   // ---------------- D setup: this wave's down-projection loads ----------------
-  // Output rows [h0, h0 + nrows); slot = (row, unit), unit fastest; RPID
-  // slots per load instruction (lane group rsD), TD segments per lane.
-  const int LI = p.LI, RPID = kWave / LI;
-  const int rsD = lane / LI, liD = lane & (LI - 1);
-  const int TD = S_I / LI;
-  const int h0 = gw * rpw;
-  const int nrows = max(0, min(H, h0 + rpw) - h0);
-  const int slots = nrows * Uall;
-  const int n_itemsD = ((slots + RPID - 1) / RPID) * TD;
   const int64_t wprD = I >> 3;
   const int64_t pprD = (QMODE == ZMOE_Q_AFFINE) ? (S_I >> p.gshift) : S_I;
-  int d_hl = rsD / Uall, d_u = rsD - (rsD / Uall) * Uall, d_t = 0, d_g = 0;
   uint4 wd[kD1D];
   RawParam rd[kD1D];
   int jhl[kD1D], ju[kD1D], jt[kD1D];
@@ -193,11 +331,10 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
         if (++d_t == TD) {
           d_t = 0;
           ++d_g;
-          d_u += RPID;
-          while (d_u >= Uall) {
-            d_u -= Uall;
-            ++d_hl;
-          }
+          const int t = d_u + RPID;
+          const int q = static_cast<int>(fdiv(static_cast<uint32_t>(t), pl.by_Uall));
+          d_hl += q;
+          d_u = t - q * Uall;
           d_u = (d_hl >= nrows) ? 0 : d_u;
         }
       }
@@ -212,17 +349,15 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
   if constexpr (XR) {
     // H = 2048: lane l owns x segment l of the row (registers), one segment
     // per lane, one wave-wide load per row.
-    const int RA = Uall * I;
-    const int per = (RA + W - 1) / W;
-    const int g0 = min(RA, gw * per), g1 = min(RA, g0 + per);
+    const int g0 = a_g0, g1 = a_g1;
     const uint4 x0 = *reinterpret_cast<const uint4*>(xs + ((0 * S_H) + lane) * 4);
     const uint4 x1 = *reinterpret_cast<const uint4*>(xs + ((1 * S_H) + lane) * 4);
     const uint4 x2 = *reinterpret_cast<const uint4*>(xs + ((2 * S_H) + lane) * 4);
     const uint4 x3 = *reinterpret_cast<const uint4*>(xs + ((3 * S_H) + lane) * 4);
     const float xsum = (QMODE == ZMOE_Q_AFFINE) ? sx[lane] : 0.0f;
     const int pi = (QMODE == ZMOE_Q_AFFINE) ? (lane >> p.gshift) : lane;
-    int cu = g0 / I;
-    int cr = g0 - cu * I;
+    int cu = a_cu;
+    int cr = a_cr;
     uint4 wg[kD1A], wu[kD1A];
     RawParam rg[kD1A], ru[kD1A];
     int jrow[kD1A], junit[kD1A];
@@ -256,10 +391,11 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
         ru[j] = seg_param_load<QMODE>(usp, ubp, poff);
       }
     };
-    // down loads first: they stream while the gate/up loads follow, and the
-    // wave's loads all return before the act rows are computed
-    load_down(0);
+    // gate/up loads first, then the down loads: loads return in order, so
+    // the gate/up rows are computed while the down bytes still stream
     if (g0 < g1) load_a(g0);
+    load_down(0);
+    if (rank_route && wave == 0) rank_weights(p, L, K);
     for (int base = g0; base < g1; base += kD1A) {
       if (base != g0) load_a(base);
       float gv[kD1A], uv[kD1A];
@@ -293,16 +429,13 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
   } else {
     // general H: LH lanes per row (RPI rows per load), T segments per lane,
     // x from LDS
-    const int LH = p.LH, RPI = kWave / LH;
-    const int rs = lane / LH, li = lane & (LH - 1);
-    const int T = S_H / LH;
-    const int rgu = I / RPI;
-    const int rg_total = Uall * rgu;
-    const int per = (rg_total + W - 1) / W;
-    const int g0 = min(rg_total, gw * per), g1 = min(rg_total, g0 + per);
-    const int n_items = (g1 - g0) * T;
-    int cu = g0 / max(rgu, 1);
-    int crg = g0 - cu * rgu;
+    const int LH = 1 << pl.lLH, RPI = kWave >> pl.lLH;
+    const int rs = lane >> pl.lLH, li = lane & (LH - 1);
+    const int T = pl.TA;
+    const int rgu = pl.rgu;
+    const int n_items = (a_g1 - a_g0) * T;
+    int cu = a_cu;
+    int crg = a_cr;
     int ct = 0;
     uint4 wg[kD1A], wu[kD1A];
     RawParam rg[kD1A], ru[kD1A];
@@ -331,8 +464,9 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
         }
       }
     };
-    load_down(0);
     if (n_items > 0) load_a(0);
+    load_down(0);
+    if (rank_route && wave == 0) rank_weights(p, L, K);
     float ag = 0.0f, au = 0.0f;
     for (int base = 0; base < n_items; base += kD1A) {
       if (base > 0) load_a(base);
@@ -390,7 +524,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
   trace_mark(p, 8);
 
   // ---------------- D: down projection ----------------
-  stage_rows_lds<QMODE, true>(p, p.act, p.act_stride, Uall, S_I, as, asx, tag16);
+  stage_rows_lds<QMODE, true>(p, p.act, p.act_stride, Uall, S_I, as, asx, tag16, p.by_S4I, p.by_SI);
   trace_mark(p, 9);
   lds_barrier();
   trace_mark(p, 10);
@@ -486,7 +620,31 @@ static int launch_d1_q(hipStream_t st, const FusedParams& fp, size_t lds, int gr
   }
 }
 
-int launch_decode1(hipStream_t st, const zmoe_layer_desc* d, const FusedParams& fp, int grid) {
+int launch_decode1(hipStream_t st, const zmoe_layer_desc* d, const FusedParams& fp_in, int grid) {
+  FusedParams fp = fp_in;
+  D1Plan& pl = fp.d1;
+  const int W = grid * kFWaves;
+  const int H = d->hidden, I = d->inter, S_H = H / 32, S_I = I / 32;
+  pl.Uall = d->top_k + (d->shared_inter > 0 ? 1 : 0);
+  pl.rpw = (H + W - 1) / W;
+  const int LH = gcd_int(S_H, kWave), LI = gcd_int(S_I, kWave);
+  pl.lLH = 0;
+  while ((1 << pl.lLH) < LH) ++pl.lLH;
+  pl.lLI = 0;
+  while ((1 << pl.lLI) < LI) ++pl.lLI;
+  pl.TA = S_H / LH;
+  pl.TD = S_I / LI;
+  pl.rgu = I / (kWave / LH);
+  pl.perA = (pl.Uall * pl.rgu + W - 1) / W;
+  pl.by_rgu = make_fastdiv(static_cast<uint32_t>(pl.rgu));
+  pl.by_Uall = make_fastdiv(static_cast<uint32_t>(pl.Uall));
+  pl.by_NC = make_fastdiv(static_cast<uint32_t>(H / 512));
+  for (int m = 0; m < 3; ++m) {
+    const int64_t N = (m == 2) ? H : I, Kin = (m == 2) ? I : H;
+    const int64_t groups = (d->quant_mode == ZMOE_Q_AFFINE) ? Kin / d->group_size : Kin / 32;
+    pl.wst[m] = N * (Kin / 8);
+    pl.sst[m] = N * groups * ((d->quant_mode == ZMOE_Q_AFFINE) ? 2 : 1);
+  }
   const size_t lds = decode1_lds_bytes(d, grid);
   const bool xr = fp.LH == kWave && fp.H == 32 * kWave;
   if (d->quant_mode == ZMOE_Q_AFFINE)

@@ -114,7 +114,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
                   (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(a));
     }
   }
-  stage_rows_lds<QMODE, false>(p, p.x, p.H, B, S_H, xs, sx, 0u);
+  stage_rows_lds<QMODE, false>(p, p.x, p.H, B, S_H, xs, sx, 0u, p.by_S4H, p.by_SH);
   trace_mark(p, 1);
   lds_barrier();
   trace_mark(p, 2);
@@ -422,7 +422,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
   float* asx = reinterpret_cast<float*>(as + static_cast<size_t>(Ptot) * lds_row_words(S_I));
   float* ybuf = asx + static_cast<size_t>(Ptot) * S_I;                         // [wg rows][Ptot]
   float* accD = ybuf + static_cast<size_t>(kFWaves) * rows_per_wave * Ptot;   // [waves][B][64]
-  stage_rows_lds<QMODE, true>(p, p.act, p.act_stride, Ptot, S_I, as, asx, tag16);
+  stage_rows_lds<QMODE, true>(p, p.act, p.act_stride, Ptot, S_I, as, asx, tag16, p.by_S4I, p.by_SI);
   lds_barrier();
   trace_mark(p, 10);
   float* ad = accD + static_cast<size_t>(wave) * B * kWave + lane;
@@ -610,6 +610,10 @@ int launch_fused(hipStream_t st, const zmoe_layer_desc* d, const void* x, int B,
   fp.out_idx = out_idx;
   fp.out_w = out_w;
   fp.trace = (d->flags & ZMOE_LAYER_TRACE) ? reinterpret_cast<unsigned long long*>(base + off_trace(d, B)) : nullptr;
+  fp.by_S4H = make_fastdiv(static_cast<uint32_t>(d->hidden / 8));
+  fp.by_SH = make_fastdiv(static_cast<uint32_t>(d->hidden / 32));
+  fp.by_S4I = make_fastdiv(static_cast<uint32_t>(d->inter / 8));
+  fp.by_SI = make_fastdiv(static_cast<uint32_t>(d->inter / 32));
   if (B == 1 && decode1_supported(d, num_cus())) return launch_decode1(st, d, fp, num_cus());
   const size_t lds = fused_lds_bytes(d, B);
   if (d->quant_mode == ZMOE_Q_AFFINE) return launch_fused_q<ZMOE_Q_AFFINE>(st, fp, lds);

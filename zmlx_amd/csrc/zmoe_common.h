@@ -68,6 +68,30 @@ __device__ __forceinline__ void dev_store(T* p, T v) {
   __hip_atomic_store((ZMOE_GLOBAL T*)(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Division by a launch-constant divisor d with a multiply-high and a shift
+// (round-up method): q = (umulhi(a, m) + a) >> s, exact for 0 <= a < 2^31.
+struct FastDiv {
+  uint32_t d, m, s;
+};
+
+__host__ inline FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f;
+  f.d = d;
+  f.s = 0;
+  while ((1ull << f.s) < d) ++f.s;
+  f.m = static_cast<uint32_t>(((1ull << 32) * ((1ull << f.s) - d)) / d + 1);
+  return f;
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t a, FastDiv f) { return (__umulhi(a, f.m) + a) >> f.s; }
+
+// Pins a wave-uniform value in a scalar register at this point of the
+// program (work assignment computed before a wait stays computed there).
+template <typename T>
+__device__ __forceinline__ void pin_s(T& x) {
+  asm volatile("" : "+s"(x));
+}
+
 // ---------------------------------------------------------------------------
 // bf16 <-> fp32
 // ---------------------------------------------------------------------------
@@ -75,15 +99,14 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b16) {
   return __uint_as_float(b16 << 16);
 }
 
+// Round to nearest even with gfx950's v_cvt_pk_bf16_f32 (one instruction;
+// NaN stays NaN, quieted).
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;  // quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 __device__ __forceinline__ float round_bf16(float f) {
-  return bf16_bits_to_f32(f32_to_bf16_bits(f));
+  return static_cast<float>(static_cast<__bf16>(f));
 }
 
 // ---------------------------------------------------------------------------

@@ -19,12 +19,24 @@ constexpr int kFMaxUnits = kFMaxB * kMaxTopK + 1;
 constexpr int kChunkA = 4;                // (row-group, segment) items per batch, phase A
 constexpr int kChunkD = 4;                // (slot-group, segment) items per batch, phase D
 constexpr unsigned kSpinLimit = 1u << 21;
-constexpr int kTraceSlots = 16;
+constexpr int kTraceSlots = 24;
 // words of the workspace's leading state block
 constexpr int kErrWord = static_cast<int>(kSyncErrorByte / 4);
 constexpr int kEpochWord = 64;  // + workgroup: launches completed
 constexpr int kMaxGrid = static_cast<int>(kSyncBlockBytes / 4) - kEpochWord;
 constexpr int kMaxNC = 16;                // router chunks of 512 (H <= 8192)
+
+// Launch constants of the one-token kernel's work assignment (host-made).
+struct D1Plan {
+  int Uall;          // routed units + shared unit
+  int rpw;           // output rows per wave (phase D)
+  int perA;          // (unit, row-group) items per wave (phase A)
+  int lLH, lLI;      // log2 of the lanes per row, K_in = H / K_in = I
+  int TA, TD;        // segments per lane, phase A / phase D
+  int rgu;           // row-groups per unit (phase A)
+  FastDiv by_rgu, by_Uall, by_NC;
+  int64_t wst[3], sst[3];  // per-expert strides: packed words, scale (= bias) bytes
+};
 
 struct FusedParams {
   int H, E, K, I, Is, B;
@@ -45,6 +57,8 @@ struct FusedParams {
   uint32_t* out_idx;
   float* out_w;
   unsigned long long* trace;  // nullable: [G][kTraceSlots] realtime stamps
+  FastDiv by_S4H, by_SH, by_S4I, by_SI;  // staged-row items: S*4 and S per row
+  D1Plan d1;
 };
 
 struct FusedLds {
@@ -125,7 +139,8 @@ __host__ __device__ constexpr int lds_row_words(int S) { return 16 * S + 32; }
 // they are.
 template <int QMODE, bool DEV>
 __device__ __forceinline__ void stage_rows_lds(const FusedParams& p, const void* __restrict__ src, int64_t src_stride,
-                                               int nrows, int S, uint32_t* xs, float* sx, unsigned tag16) {
+                                               int nrows, int S, uint32_t* xs, float* sx, unsigned tag16,
+                                               FastDiv by_S4, FastDiv by_S) {
   // all (row, segment, quarter) items at once, two per thread per round, so
   // the loads of every row are in flight together
   const int S4 = S * 4;
@@ -139,7 +154,7 @@ __device__ __forceinline__ void stage_rows_lds(const FusedParams& p, const void*
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int i = min(i0 + h * kFThreads, n - 1);  // past the end: repeat a valid item
-        const int r = i / S4, rem = i - r * S4;
+        const int r = fdiv(i, by_S4), rem = i - r * S4;
         q[h] = static_cast<const uint32_t*>(src) + r * src_stride + rem * 8;
       }
       uint4 w[2][2];
@@ -183,7 +198,7 @@ __device__ __forceinline__ void stage_rows_lds(const FusedParams& p, const void*
       for (int h = 0; h < 2; ++h) {
         const int i = i0 + h * kFThreads;
         if (i < n) {
-          const int r = i / S4, rem = i - r * S4;
+          const int r = fdiv(i, by_S4), rem = i - r * S4;
           v[h] = gload(reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(src) + r * src_stride + rem * 8));
         }
       }
@@ -192,7 +207,7 @@ __device__ __forceinline__ void stage_rows_lds(const FusedParams& p, const void*
     for (int h = 0; h < 2; ++h) {
       const int i = i0 + h * kFThreads;
       if (i < n) {
-        const int r = i / S4, rem = i - r * S4;
+        const int r = fdiv(i, by_S4), rem = i - r * S4;
         const int s = rem >> 2, j = rem & 3;
         uint4 o;
         if (QMODE == ZMOE_Q_AFFINE) {
@@ -210,7 +225,7 @@ __device__ __forceinline__ void stage_rows_lds(const FusedParams& p, const void*
   if (QMODE == ZMOE_Q_AFFINE) {
     lds_barrier();
     for (int i = threadIdx.x; i < nrows * S; i += kFThreads) {
-      const int r = i / S, s = i - r * S;
+      const int r = fdiv(i, by_S), s = i - r * S;
       float acc = 0.0f;
       for (int w = 0; w < 4; ++w) {
         // pairs (e0,e4) (e1,e5) (e2,e6) (e3,e7) summed in natural order:
