@@ -198,9 +198,9 @@ def _layer_pair(dev, rng, family, *, H, E, I, K, mode="affine", gs=64, shared_I=
 
 
 FUSED_CASES = [
-    ("qwen3", dict(H=2048, E=128, I=768, K=8), [1, 4, 8]),
-    ("lfm2", dict(H=2048, E=32, I=1792, K=4), [1, 3]),
-    ("glm", dict(H=2048, E=64, I=1536, K=4, mode="mxfp4", gs=32, shared_I=1536), [1, 8]),
+    ("qwen3", dict(H=2048, E=128, I=768, K=8), [1, 2, 4, 8, 16, 5]),
+    ("lfm2", dict(H=2048, E=32, I=1792, K=4), [1, 3, 16]),
+    ("glm", dict(H=2048, E=64, I=1536, K=4, mode="mxfp4", gs=32, shared_I=1536), [1, 8, 16, 2]),
     ("deepseek", dict(H=1024, E=256, I=512, K=8, shared_I=512), [1, 2]),
 ]
 

@@ -504,6 +504,8 @@ size_t fused_lds_bytes(const zmoe_layer_desc* d, int B) {
 }
 
 bool fused_supported(const zmoe_layer_desc* d, int B) {
+  if (num_cus() > kMaxGrid) return false;
+  if (B >= 2 && decodeb_supported(d, B, num_cus())) return true;
   if (B < 1 || B > kFMaxB) return false;
   if (num_cus() > kMaxGrid) return false;
   if (d->hidden % 512 != 0 || d->hidden / 512 > kMaxNC) return false;
@@ -615,6 +617,7 @@ int launch_fused(hipStream_t st, const zmoe_layer_desc* d, const void* x, int B,
   fp.by_S4I = make_fastdiv(static_cast<uint32_t>(d->inter / 8));
   fp.by_SI = make_fastdiv(static_cast<uint32_t>(d->inter / 32));
   if (B == 1 && decode1_supported(d, num_cus())) return launch_decode1(st, d, fp, num_cus());
+  if (B >= 2 && decodeb_supported(d, B, num_cus())) return launch_decodeb(st, d, fp, num_cus());
   const size_t lds = fused_lds_bytes(d, B);
   if (d->quant_mode == ZMOE_Q_AFFINE) return launch_fused_q<ZMOE_Q_AFFINE>(st, fp, lds);
   return launch_fused_q<ZMOE_Q_MXFP4>(st, fp, lds);

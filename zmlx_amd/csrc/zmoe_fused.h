@@ -34,7 +34,8 @@ struct D1Plan {
   int lLH, lLI;      // log2 of the lanes per row, K_in = H / K_in = I
   int TA, TD;        // segments per lane, phase A / phase D
   int rgu;           // row-groups per unit (phase A)
-  FastDiv by_rgu, by_Uall, by_NC;
+  int PB;             // act slots per down-projection pass (batched kernel)
+  FastDiv by_rgu, by_Uall, by_NC, by_W, by_I;
   int64_t wst[3], sst[3];  // per-expert strides: packed words, scale (= bias) bytes
 };
 
@@ -137,29 +138,29 @@ __host__ __device__ constexpr int lds_row_words(int S) { return 16 * S + 32; }
 // workgroups of an XCD then share one fetch through its L2), and every item
 // whose tags are not all current is re-read with device-coherent loads until
 // they are.
-template <int QMODE, bool DEV>
+template <int QMODE, bool DEV, int NI = 2>
 __device__ __forceinline__ void stage_rows_lds(const FusedParams& p, const void* __restrict__ src, int64_t src_stride,
                                                int nrows, int S, uint32_t* xs, float* sx, unsigned tag16,
                                                FastDiv by_S4, FastDiv by_S) {
-  // all (row, segment, quarter) items at once, two per thread per round, so
-  // the loads of every row are in flight together
+  // (row, segment, quarter) items, NI per thread per round, all of a round's
+  // loads in flight together
   const int S4 = S * 4;
   const int RW = lds_row_words(S);
   const int n = nrows * S4;
-  for (int i0 = threadIdx.x; i0 < n; i0 += 2 * kFThreads) {
-    uint4 v[2];
+  for (int i0 = threadIdx.x; i0 < n; i0 += NI * kFThreads) {
+    uint4 v[NI];
     if (DEV) {
       const uint32_t want = tag16 << 16;
-      const uint32_t* q[2];
+      const uint32_t* q[NI];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < NI; ++h) {
         const int i = min(i0 + h * kFThreads, n - 1);  // past the end: repeat a valid item
         const int r = fdiv(i, by_S4), rem = i - r * S4;
         q[h] = static_cast<const uint32_t*>(src) + r * src_stride + rem * 8;
       }
-      uint4 w[2][2];
+      uint4 w[NI][2];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < NI; ++h) {
         w[h][0] = gload(reinterpret_cast<const uint4*>(q[h]));
         w[h][1] = gload(reinterpret_cast<const uint4*>(q[h]) + 1);
       }
@@ -171,14 +172,14 @@ __device__ __forceinline__ void stage_rows_lds(const FusedParams& p, const void*
       for (;;) {
         bool ok = true;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) ok = ok && current(w[h][0]) && current(w[h][1]);
+        for (int h = 0; h < NI; ++h) ok = ok && current(w[h][0]) && current(w[h][1]);
         if (ok) break;
         if (++spins > kSpinLimit) {
           wait_timeout(p);
           break;
         }
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < NI; ++h) {
           unsigned long long d[4];
 #pragma unroll
           for (int k = 0; k < 4; ++k) d[k] = dev_load(reinterpret_cast<const unsigned long long*>(q[h]) + k);
@@ -190,12 +191,12 @@ __device__ __forceinline__ void stage_rows_lds(const FusedParams& p, const void*
       }
       auto pair = [](uint32_t lo, uint32_t hi) { return (lo & 0xFFFFu) | (hi << 16); };
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+      for (int h = 0; h < NI; ++h)
         v[h] = make_uint4(pair(w[h][0].x, w[h][0].y), pair(w[h][0].z, w[h][0].w), pair(w[h][1].x, w[h][1].y),
                           pair(w[h][1].z, w[h][1].w));
     } else {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < NI; ++h) {
         const int i = i0 + h * kFThreads;
         if (i < n) {
           const int r = fdiv(i, by_S4), rem = i - r * S4;
@@ -204,7 +205,7 @@ __device__ __forceinline__ void stage_rows_lds(const FusedParams& p, const void*
       }
     }
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < NI; ++h) {
       const int i = i0 + h * kFThreads;
       if (i < n) {
         const int r = fdiv(i, by_S4), rem = i - r * S4;
@@ -286,5 +287,9 @@ __device__ __forceinline__ void seg_param_decode(RawParam r, float& s, float& c)
 // supports the shape (ZMOE_DECODE1=0 in the environment turns it off).
 bool decode1_supported(const zmoe_layer_desc* d, int grid);
 int launch_decode1(hipStream_t st, const zmoe_layer_desc* d, const FusedParams& fp, int grid);
+// Batched kernel (decodeb.hip): 2 <= B <= 16 at hidden 2048
+// (ZMOE_DECODEB=0 turns it off).
+bool decodeb_supported(const zmoe_layer_desc* d, int B, int grid);
+int launch_decodeb(hipStream_t st, const zmoe_layer_desc* d, const FusedParams& fp, int grid);
 
 }  // namespace zmoe
