@@ -148,6 +148,44 @@ def unique_experts(layers, x):
     return counts, idxs
 
 
+def prefill_x(layer, B, gen, dev, skew=1.1, peak=3.0, seed=7):
+    """x for the prefill line (config 4): N(0,1) tokens plus a shared
+    component along the router rows that adds a Zipf-skewed logit offset
+    peak * rank^-skew to the experts (ranks over a fixed random permutation),
+    so expert loads are imbalanced."""
+    import torch
+
+    wr = layer._router_w.float()
+    rank = torch.empty(E, device=dev)
+    perm = torch.randperm(E, generator=torch.Generator().manual_seed(seed)).to(dev)
+    rank[perm] = torch.arange(1, E + 1, device=dev, dtype=torch.float32)
+    off = peak * rank.pow(-skew)
+    v = ((off / (wr * wr).sum(1))[:, None] * wr).sum(0)
+    z = torch.randn((B, H), generator=gen, device=dev)
+    return (z + v[None, :]).to(torch.bfloat16)
+
+
+def prefill_line(layers, B, gen, dev, steps, warmup):
+    """Config 4: B tokens through every layer copy (grouped GEMMs on MFMA over
+    the pairs sorted by expert), graph-replayed like the decode lines."""
+    x = prefill_x(layers[0], B, gen, dev)
+    counts, idxs = unique_experts(layers, x)
+    import torch
+
+    loads = torch.bincount(idxs[0].reshape(-1).long(), minlength=E).cpu().tolist()
+    ms = time_layers(layers, x, steps, warmup)
+    layer_us = ms * 1e3 / len(layers)
+    avg_unique = sum(counts) / len(counts)
+    alg_bytes = avg_unique * per_expert_bytes() + E * H * 2 + 4 * B * H
+    flops = B * K * 6 * H * I + 2 * B * E * H
+    gbps = alg_bytes / (layer_us * 1e-6) / 1e9
+    return {"tokens": B, "us_per_layer_call": round(layer_us, 3), "us_per_token": round(layer_us / B, 4),
+            "gbps": round(gbps, 1), "roofline_frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "tflops": round(flops / (layer_us * 1e-6) / 1e12, 2), "mfma_frac_bf16": round(flops / (layer_us * 1e-6) / 2.5e15, 4),
+            "unique_experts": round(avg_unique, 2), "max_expert_rows": max(loads), "min_expert_rows": min(loads),
+            "alg_bytes_per_call": int(alg_bytes), "steps": steps}
+
+
 def load_traffic():
     """HBM bytes per k_moe_decode launch measured by rocprofv3 (FETCH_SIZE and
     WRITE_SIZE, calibrated on a copy kernel), if the summary is committed."""
@@ -259,6 +297,8 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--extra-batches", default="4,16")
+    ap.add_argument("--prefill", type=int, default=512,
+                    help="tokens of the prefill line (config 4; 0 skips it)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
@@ -314,9 +354,15 @@ def main() -> int:
             roof = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                     "frac": round(gbps / HBM_PEAK_GBPS, 4),
                     "traffic": int(tr["bytes_per_launch"]) if tr else None,
-                    "kernel": "k_moe_decode (single-launch MoE layer)", "avg_launch_us": round(layer_us, 3),
+                    "kernel": "k_moe_decode1 (one-token single-launch MoE layer)" if B == 1 else
+                              "k_moe_decodeb (batched single-launch MoE layer)",
+                    "avg_launch_us": round(layer_us, 3),
                     "alg_bytes_per_launch": int(alg_bytes)}
         log(f"B={B}: {rec}")
+
+    if args.prefill > 0:
+        per_b["prefill"] = prefill_line(layers, args.prefill, gen, dev, max(3, args.steps // 10), args.warmup)
+        log(f"prefill: {per_b['prefill']}")
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -139,6 +139,55 @@ def test_layer_glm_mxfp4_shared(dev, B):
     _cmp_out(from_dev(out), ref)
 
 
+@pytest.mark.parametrize("B", [32, 64])
+def test_layer_prefill_grouped_qwen3(dev, B):
+    """Prefill-sized batches (>= 32 tokens) run the routed experts as grouped
+    GEMMs on MFMA (pairs sorted by expert): Qwen3 per-expert shapes, 32
+    experts, checked against the oracle like the decode batches."""
+    import torch
+
+    from zmlx_amd.layer import QuantizedMoELayer
+
+    rng = np.random.default_rng(500 + B)
+    H, E, I, K = 2048, 32, 768, 8
+    banks, wr, sh, tq, tsh, wr_t = _build(dev, rng, H=H, E=E, I=I, K=K)
+    layer = QuantizedMoELayer.for_family("qwen3", wr_t, tq["gate"], tq["up"], tq["down"], top_k=K)
+    x = bf16_randn(rng, (B, H))
+    out, idx, w = layer(to_bf16(x, dev), return_routing=True)
+    torch.cuda.synchronize()
+    idx = from_dev(idx).astype(np.int64)
+    logits = O.dense_logits(x, wr)
+    assert O.topk_is_valid(idx, O.softmax_precise_bf16(logits), K).all()
+    _, w_ref, _ = O.qwen_gating(logits, K, True, idx=idx)
+    assert O.bf16_ulp_diff(from_dev(w), w_ref).max() <= 1
+    ref = _oracle_out(x, idx, O.bf16_round(from_dev(w)), banks, None, "affine", 64, "native")
+    _cmp_out(from_dev(out), ref)
+
+
+def test_layer_prefill_grouped_glm_mxfp4_shared(dev):
+    """Grouped MFMA experts with mxfp4 weights, the sigmoid router and the
+    shared expert at a prefill-sized batch (40 tokens)."""
+    import torch
+
+    from zmlx_amd.layer import QuantizedMoELayer
+
+    rng = np.random.default_rng(640)
+    H, E, I, K, B = 2048, 64, 1536, 4, 40
+    banks, wr, sh, tq, tsh, wr_t = _build(dev, rng, H=H, E=E, I=I, K=K, mode="mxfp4", gs=32, shared_I=1536)
+    bias = (rng.standard_normal(E) * 0.05).astype(np.float32)
+    layer = QuantizedMoELayer.for_family("glm", wr_t, tq["gate"], tq["up"], tq["down"], top_k=K,
+                                         router_bias=torch.from_numpy(bias).to(dev), group_size=32, mode="mxfp4",
+                                         routed_scaling_factor=1.8, shared=tsh)
+    x = bf16_randn(rng, (B, H))
+    out, idx, w = layer(to_bf16(x, dev), return_routing=True)
+    torch.cuda.synchronize()
+    logits = O.dense_logits(x, wr)
+    w_ref, i_ref = O.deepseek_router_topk_sigmoid(logits, bias, K, 1, 1, 1.8)
+    np.testing.assert_array_equal(from_dev(idx), i_ref)
+    ref = _oracle_out(x, i_ref, w_ref, banks, sh, "mxfp4", 32, "fp32_no_fma")
+    _cmp_out(from_dev(out), ref)
+
+
 def test_layer_deepseek_grouped(dev):
     """DeepSeek-V3 routing (256 experts, 8 groups, top-4 groups, top-8,
     scale 2.5) with reduced H/I for oracle speed; shared expert."""

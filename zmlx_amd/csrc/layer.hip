@@ -3,6 +3,7 @@
 // enqueued back to back on one stream with all intermediates in the
 // caller's workspace.
 #include "zmoe_common.h"
+#include "zmoe_grouped.h"
 #include "zmoe_host.h"
 
 #include <cstdlib>
@@ -12,6 +13,26 @@ namespace zmoe {
 
 static size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
+// Batches of at least this many tokens run the routed experts as grouped
+// GEMMs on MFMA (pairs sorted by expert; the reference's mlx_lm SwitchGLU
+// sorts from 64 indices on, moe_mlp.py:540-543); smaller ones as GEMVs.
+// ZMOE_GROUPED_MIN_B overrides it.
+constexpr int kGroupedMinB = 32;
+
+static int grouped_min_b() {
+  static int v = -1;
+  if (v < 0) {
+    const char* e = getenv("ZMOE_GROUPED_MIN_B");
+    v = e ? atoi(e) : kGroupedMinB;
+    if (v < 1) v = 1;
+  }
+  return v;
+}
+
+static bool use_grouped(const zmoe_layer_desc* d, int B) {
+  return B >= grouped_min_b() && d->hidden % 128 == 0 && d->inter % 128 == 0 && d->n_experts <= 1024;
+}
+
 struct LayerWs {
   void* logits;   // [B, E] bf16
   uint32_t* idx;  // [B, K]
@@ -20,6 +41,10 @@ struct LayerWs {
   void* y;        // [B*K, H] bf16
   void* sh_act;   // [B, I_s] bf16
   void* sh_y;     // [B, H] bf16
+  int* offsets;   // grouped path: [E+1] pair ranges by expert
+  int* sorted;    //   [B*K] pairs in expert order
+  float* xsum;    //   affine: [B][H/gs] group sums of x
+  float* asum;    //   affine: [B*K][I/gs] group sums of act
   size_t bytes;
 };
 
@@ -39,6 +64,13 @@ static LayerWs layout_ws(const zmoe_layer_desc* d, int B, char* base) {
   ws.y = take(BK * d->hidden * 2);
   ws.sh_act = take(static_cast<size_t>(B) * (d->shared_inter > 0 ? d->shared_inter : 0) * 2);
   ws.sh_y = take(static_cast<size_t>(B) * (d->shared_inter > 0 ? d->hidden : 0) * 2);
+  if (use_grouped(d, B)) {
+    const int gs = d->group_size > 0 ? d->group_size : 32;
+    ws.offsets = static_cast<int*>(take(static_cast<size_t>(d->n_experts + 1) * 4));
+    ws.sorted = static_cast<int*>(take(BK * 4));
+    ws.xsum = static_cast<float*>(take(static_cast<size_t>(B) * (d->hidden / gs) * 4));
+    ws.asum = static_cast<float*>(take(BK * (d->inter / gs) * 4));
+  }
   ws.bytes = off;
   return ws;
 }
@@ -153,12 +185,68 @@ extern "C" int zmoe_moe_layer(void* stream, const zmoe_layer_desc* d, const void
   }
   if (rc) return rc;
   // 3. routed experts: gate/up + SwiGLU, then down
-  rc = dispatch_qmv(true, stream, x, d->gate_w, d->gate_s, d->gate_b, d->up_w, d->up_s, d->up_b, nullptr, ws.idx, K,
-                    static_cast<int64_t>(B) * K, 1, I, H, d->quant_mode, gshift, ws.act);
-  if (rc) return rc;
-  rc = dispatch_qmv(false, stream, ws.act, d->down_w, d->down_s, d->down_b, nullptr, nullptr, nullptr, nullptr, ws.idx,
-                    1, static_cast<int64_t>(B) * K, 1, H, I, d->quant_mode, gshift, ws.y);
-  if (rc) return rc;
+  if (use_grouped(d, B)) {
+    // grouped GEMMs on MFMA over the (token, k) pairs sorted by expert; act
+    // and y stay in pair order
+    const int npairs = B * K;
+    const bool affine = d->quant_mode == ZMOE_Q_AFFINE;
+    rc = launch_sort_pairs(st, ws.idx, npairs, E, ws.offsets, ws.sorted);
+    if (rc) return rc;
+    if (affine) {
+      rc = launch_row_group_sums(st, static_cast<const uint16_t*>(x), H, B, H, d->group_size, ws.xsum);
+      if (rc) return rc;
+    }
+    GroupedArgs g{};
+    g.a = static_cast<const uint16_t*>(x);
+    g.lda = H;
+    g.asum = ws.xsum;
+    g.offsets = ws.offsets;
+    g.sorted = ws.sorted;
+    g.lhs = nullptr;
+    g.a_div = K;  // pair (b, k) reads token b
+    g.scatter = 1;
+    g.M = npairs;
+    g.w0 = d->gate_w;
+    g.s0 = d->gate_s;
+    g.b0 = d->gate_b;
+    g.w1 = d->up_w;
+    g.s1 = d->up_s;
+    g.b1 = d->up_b;
+    g.N = I;
+    g.K = H;
+    g.gs = d->group_size;
+    g.out = static_cast<uint16_t*>(ws.act);
+    g.ldo = I;
+    rc = launch_grouped(st, g, E, d->quant_mode, true);
+    if (rc) return rc;
+    if (affine) {
+      rc = launch_row_group_sums(st, static_cast<const uint16_t*>(ws.act), I, npairs, I, d->group_size, ws.asum);
+      if (rc) return rc;
+    }
+    g.a = static_cast<const uint16_t*>(ws.act);
+    g.lda = I;
+    g.asum = ws.asum;
+    g.a_div = 1;  // pair p reads act row p
+    g.w0 = d->down_w;
+    g.s0 = d->down_s;
+    g.b0 = d->down_b;
+    g.w1 = nullptr;
+    g.s1 = nullptr;
+    g.b1 = nullptr;
+    g.N = H;
+    g.K = I;
+    g.out = static_cast<uint16_t*>(ws.y);
+    g.ldo = H;
+    rc = launch_grouped(st, g, E, d->quant_mode, false);
+    if (rc) return rc;
+  } else {
+    rc = dispatch_qmv(true, stream, x, d->gate_w, d->gate_s, d->gate_b, d->up_w, d->up_s, d->up_b, nullptr, ws.idx, K,
+                      static_cast<int64_t>(B) * K, 1, I, H, d->quant_mode, gshift, ws.act);
+    if (rc) return rc;
+    rc = dispatch_qmv(false, stream, ws.act, d->down_w, d->down_s, d->down_b, nullptr, nullptr, nullptr, nullptr,
+                      ws.idx, 1, static_cast<int64_t>(B) * K, 1, H, I, d->quant_mode, gshift, ws.y);
+    if (rc) return rc;
+  }
   // 4. shared expert (dense SwiGLU MLP on every token)
   const void* shared = nullptr;
   if (d->shared_inter > 0) {
