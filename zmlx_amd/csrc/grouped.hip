@@ -47,7 +47,8 @@ constexpr int kGTileM = 32;     // sorted rows per MFMA block
 // sort (token, k) pairs by expert: one workgroup, counts in LDS
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void k_sort_pairs(const uint32_t* __restrict__ idx, int npairs, int E,
-                                                     int* __restrict__ offsets, int* __restrict__ sorted) {
+                                                     int* __restrict__ offsets, int* __restrict__ sorted,
+                                                     int* __restrict__ blocks) {
   __shared__ int cnt[1024];
   __shared__ int off[1025];
   for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
@@ -64,6 +65,23 @@ __global__ __launch_bounds__(1024) void k_sort_pairs(const uint32_t* __restrict_
   }
   __syncthreads();
   for (int e = threadIdx.x; e <= E; e += blockDim.x) offsets[e] = off[e];
+  if (blocks) {
+    // 32-row blocks of every expert, in expert order (their starts reuse cnt)
+    if (threadIdx.x == 0) {
+      int nb = 0;
+      for (int e = 0; e < E; ++e) {
+        cnt[e] = nb;
+        nb += (off[e + 1] - off[e] + 31) / 32;
+      }
+      offsets[E + 1] = nb;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+      const int nbe = (off[e + 1] - off[e] + 31) / 32;
+      for (int j = 0; j < nbe; ++j) blocks[cnt[e] + j] = e | (j << 11);
+    }
+    __syncthreads();
+  }
   for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
   __syncthreads();
   // position inside an expert's range is arbitrary: every row is computed
@@ -139,15 +157,30 @@ __device__ __forceinline__ float group_scale(const void* s, int64_t i) {
 template <int QMODE, bool G32, bool SWIGLU>
 __global__ __launch_bounds__(kGThreads) void k_grouped_qmm(GroupedArgs g) {
   const int ntiles = (g.N + kGTileN - 1) / kGTileN;
-  const int e = blockIdx.x / ntiles;
-  const int tile = blockIdx.x - e * ntiles;
   const int wave = threadIdx.x / kWave;
   const int lane = __lane_id();
   const int h = lane >> 5, col = lane & 31;
+  // workgroup -> (expert, 32-row blocks, 128-row output tile): one block per
+  // workgroup from the block list (heavy experts spread over many
+  // workgroups), else every block of expert blockIdx / ntiles
+  int e, tile, m_first, m_last;
+  if (g.blocks) {
+    const int b = blockIdx.x / ntiles;
+    tile = blockIdx.x - b * ntiles;
+    if (b >= g.offsets[g.E + 1]) return;
+    const int be = g.blocks[b];
+    e = be & 2047;
+    m_first = g.offsets[e] + (be >> 11) * kGTileM;
+    m_last = min(m_first + kGTileM, g.offsets[e + 1]);
+  } else {
+    e = blockIdx.x / ntiles;
+    tile = blockIdx.x - e * ntiles;
+    m_first = g.offsets ? g.offsets[e] : 0;
+    m_last = g.offsets ? g.offsets[e + 1] : g.M;
+  }
   const int n0 = tile * kGTileN + wave * 32;
   if (n0 >= g.N) return;
-  const int r_begin = g.offsets ? g.offsets[e] : 0;
-  const int r_end = g.offsets ? g.offsets[e + 1] : g.M;
+  const int r_begin = m_first, r_end = g.offsets ? (g.blocks ? m_last : g.offsets[e + 1]) : g.M;
   if (r_begin >= r_end) return;
 
   const AffineK ak = affine_k();
@@ -174,39 +207,83 @@ __global__ __launch_bounds__(kGThreads) void k_grouped_qmm(GroupedArgs g) {
     f32x16_t acc0 = {}, acc1 = {};
     int ks = 0;  // k-steps into the current group
     int grp = 0;
-    for (int blk = 0; blk < nblk; ++blk) {
+    const float* as_row = (QMODE == ZMOE_Q_AFFINE) ? g.asum + arow * G : nullptr;
+    // Per 64-k block: weights, activations, the scales of the groups this
+    // block completes (gs 32: two, 64: one, 128: one every other block) and
+    // the operands of one affine-offset step (two groups per f32 MFMA,
+    // G / 2 <= blocks), all loaded one block ahead of their use.
+    struct KBuf {
       uint32_t w0[4], w1[4];
       uint4 av[4];
+      uint32_t s0[2], s1[2];  // raw scales
+      float xs;               // offset step: group sum of a
+      uint32_t os0, ob0, os1, ob1;  // offset step: raw scale / bias
+    };
+    const int gpb2 = 128 / g.gs;  // groups completed per 2 blocks
+    const int nsteps = G >> 1;
+    auto raw_scale = [&](const void* sp, int64_t i) -> uint32_t {
+      if (QMODE == ZMOE_Q_AFFINE) return gload(static_cast<const uint16_t*>(sp) + i);
+      return gload(static_cast<const uint8_t*>(sp) + i);
+    };
+    auto load_blk = [&](int blk, KBuf& kb) {
       if (!G32) {
         const uint4 q0 = gload(reinterpret_cast<const uint4*>(W0 + blk * 8 + h * 4));
-        w0[0] = q0.x, w0[1] = q0.y, w0[2] = q0.z, w0[3] = q0.w;
+        kb.w0[0] = q0.x, kb.w0[1] = q0.y, kb.w0[2] = q0.z, kb.w0[3] = q0.w;
         if (SWIGLU) {
           const uint4 q1 = gload(reinterpret_cast<const uint4*>(W1 + blk * 8 + h * 4));
-          w1[0] = q1.x, w1[1] = q1.y, w1[2] = q1.z, w1[3] = q1.w;
+          kb.w1[0] = q1.x, kb.w1[1] = q1.y, kb.w1[2] = q1.z, kb.w1[3] = q1.w;
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) av[j] = gload(reinterpret_cast<const uint4*>(A + blk * 64 + h * 32 + j * 8));
+        for (int j = 0; j < 4; ++j) kb.av[j] = gload(reinterpret_cast<const uint4*>(A + blk * 64 + h * 32 + j * 8));
       } else {
         const uint4 qa = gload(reinterpret_cast<const uint4*>(W0 + blk * 8));
         const uint4 qb = gload(reinterpret_cast<const uint4*>(W0 + blk * 8 + 4));
-        w0[0] = h ? qa.y : qa.x, w0[1] = h ? qa.w : qa.z, w0[2] = h ? qb.y : qb.x, w0[3] = h ? qb.w : qb.z;
+        kb.w0[0] = h ? qa.y : qa.x, kb.w0[1] = h ? qa.w : qa.z, kb.w0[2] = h ? qb.y : qb.x, kb.w0[3] = h ? qb.w : qb.z;
         if (SWIGLU) {
           const uint4 ua = gload(reinterpret_cast<const uint4*>(W1 + blk * 8));
           const uint4 ub = gload(reinterpret_cast<const uint4*>(W1 + blk * 8 + 4));
-          w1[0] = h ? ua.y : ua.x, w1[1] = h ? ua.w : ua.z, w1[2] = h ? ub.y : ub.x, w1[3] = h ? ub.w : ub.z;
+          kb.w1[0] = h ? ua.y : ua.x, kb.w1[1] = h ? ua.w : ua.z, kb.w1[2] = h ? ub.y : ub.x,
+          kb.w1[3] = h ? ub.w : ub.z;
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) av[j] = gload(reinterpret_cast<const uint4*>(A + blk * 64 + (2 * j + h) * 8));
+        for (int j = 0; j < 4; ++j) kb.av[j] = gload(reinterpret_cast<const uint4*>(A + blk * 64 + (2 * j + h) * 8));
       }
+      // groups completed in this block: [first, first + cnt)
+      const int first = (blk * gpb2) >> 1;
+      const int cnt = (((blk + 1) * gpb2) >> 1) - first;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int gi = min(first + i, G - 1);
+        kb.s0[i] = i < cnt ? raw_scale(g.s0, prow + gi) : 0u;
+        if (SWIGLU) kb.s1[i] = i < cnt ? raw_scale(g.s1, prow + gi) : 0u;
+      }
+      if (QMODE == ZMOE_Q_AFFINE) {
+        const int gi = min(2 * blk + h, G - 1);
+        const bool ok = blk < nsteps && 2 * blk + h < G;
+        kb.xs = ok ? as_row[gi] : 0.0f;
+        kb.os0 = ok ? gload(static_cast<const uint16_t*>(g.s0) + prow + gi) : 0u;
+        kb.ob0 = ok ? gload(static_cast<const uint16_t*>(g.b0) + prow + gi) : 0u;
+        if (SWIGLU) {
+          kb.os1 = ok ? gload(static_cast<const uint16_t*>(g.s1) + prow + gi) : 0u;
+          kb.ob1 = ok ? gload(static_cast<const uint16_t*>(g.b1) + prow + gi) : 0u;
+        }
+      }
+    };
+    auto decode_scale = [&](uint32_t r) -> float {
+      if (QMODE == ZMOE_Q_AFFINE) return bf16_bits_to_f32(r);
+      return e8m0_to_f32(r);
+    };
+    auto compute_blk = [&](int blk, const KBuf& kb) {
+      int done = 0;  // groups completed so far in this block
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const bf16x8_t xa = (QMODE == ZMOE_Q_AFFINE) ? act_affine(av[j]) : act_natural(av[j]);
-        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa, wt_operand<QMODE>(w0[j], ak), acc0, 0, 0, 0);
-        if (SWIGLU) acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa, wt_operand<QMODE>(w1[j], ak), acc1, 0, 0, 0);
+        const bf16x8_t xa = (QMODE == ZMOE_Q_AFFINE) ? act_affine(kb.av[j]) : act_natural(kb.av[j]);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa, wt_operand<QMODE>(kb.w0[j], ak), acc0, 0, 0, 0);
+        if (SWIGLU) acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa, wt_operand<QMODE>(kb.w1[j], ak), acc1, 0, 0, 0);
         if (++ks == kpg) {  // group complete: scale into the totals
           ks = 0;
-          const float s0 = group_scale<QMODE>(g.s0, prow + grp);
-          const float s1 = SWIGLU ? group_scale<QMODE>(g.s1, prow + grp) : 0.0f;
+          const float s0 = decode_scale(done == 0 ? kb.s0[0] : kb.s0[1]);
+          const float s1 = SWIGLU ? decode_scale(done == 0 ? kb.s1[0] : kb.s1[1]) : 0.0f;
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             tot0[i] = fmaf(s0, acc0[i], tot0[i]);
@@ -217,27 +294,28 @@ __global__ __launch_bounds__(kGThreads) void k_grouped_qmm(GroupedArgs g) {
             }
           }
           ++grp;
+          ++done;
         }
       }
-    }
-    if (QMODE == ZMOE_Q_AFFINE) {
-      // + sum_g (b_g - 128 s_g) * asum_g, two groups per f32 MFMA
-      const float* as = g.asum + arow * G;
-      for (int t = 0; t < G; t += 2) {
-        const int gi = t + h;
-        const bool ok = gi < G;
-        const float xs = ok ? as[gi] : 0.0f;
-        float c0 = 0.0f, c1 = 0.0f;
-        if (ok) {
-          const float s = bf16_bits_to_f32(gload(static_cast<const uint16_t*>(g.s0) + prow + gi));
-          c0 = bf16_bits_to_f32(gload(static_cast<const uint16_t*>(g.b0) + prow + gi)) - 128.0f * s;
-          if (SWIGLU) {
-            const float su = bf16_bits_to_f32(gload(static_cast<const uint16_t*>(g.s1) + prow + gi));
-            c1 = bf16_bits_to_f32(gload(static_cast<const uint16_t*>(g.b1) + prow + gi)) - 128.0f * su;
-          }
+      if (QMODE == ZMOE_Q_AFFINE && blk < nsteps) {
+        // + (b_g - 128 s_g) * asum_g for groups 2 blk, 2 blk + 1
+        const float c0 = bf16_bits_to_f32(kb.ob0) - 128.0f * bf16_bits_to_f32(kb.os0);
+        tot0 = __builtin_amdgcn_mfma_f32_32x32x2f32(kb.xs, c0, tot0, 0, 0, 0);
+        if (SWIGLU) {
+          const float c1 = bf16_bits_to_f32(kb.ob1) - 128.0f * bf16_bits_to_f32(kb.os1);
+          tot1 = __builtin_amdgcn_mfma_f32_32x32x2f32(kb.xs, c1, tot1, 0, 0, 0);
         }
-        tot0 = __builtin_amdgcn_mfma_f32_32x32x2f32(xs, c0, tot0, 0, 0, 0);
-        if (SWIGLU) tot1 = __builtin_amdgcn_mfma_f32_32x32x2f32(xs, c1, tot1, 0, 0, 0);
+      }
+    };
+    // next block's loads in flight while the current one runs on MFMA
+    KBuf kb0, kb1;
+    load_blk(0, kb0);
+    for (int blk = 0; blk < nblk; blk += 2) {
+      if (blk + 1 < nblk) load_blk(blk + 1, kb1);
+      compute_blk(blk, kb0);
+      if (blk + 1 < nblk) {
+        if (blk + 2 < nblk) load_blk(blk + 2, kb0);
+        compute_blk(blk + 1, kb1);
       }
     }
     // epilogue: element i is row (i/4)*8 + h*4 + i%4 of the block, column n
@@ -259,7 +337,8 @@ __global__ __launch_bounds__(kGThreads) void k_grouped_qmm(GroupedArgs g) {
 template <int QMODE, bool G32, bool SWIGLU>
 static void launch_grouped_t(hipStream_t st, const GroupedArgs& g, int n_experts) {
   const int ntiles = (g.N + kGTileN - 1) / kGTileN;
-  hipLaunchKernelGGL((k_grouped_qmm<QMODE, G32, SWIGLU>), dim3(n_experts * ntiles), dim3(kGThreads), 0, st, g);
+  const int units = g.blocks ? grouped_max_blocks(g.M, n_experts) : n_experts;
+  hipLaunchKernelGGL((k_grouped_qmm<QMODE, G32, SWIGLU>), dim3(units * ntiles), dim3(kGThreads), 0, st, g);
 }
 
 int launch_grouped(hipStream_t st, const GroupedArgs& g, int n_experts, int quant_mode, bool swiglu) {
@@ -278,8 +357,8 @@ int launch_grouped(hipStream_t st, const GroupedArgs& g, int n_experts, int quan
   return check_launch("grouped gather_qmm");
 }
 
-int launch_sort_pairs(hipStream_t st, const uint32_t* idx, int npairs, int E, int* offsets, int* sorted) {
-  hipLaunchKernelGGL(k_sort_pairs, dim3(1), dim3(1024), 0, st, idx, npairs, E, offsets, sorted);
+int launch_sort_pairs(hipStream_t st, const uint32_t* idx, int npairs, int E, int* offsets, int* sorted, int* blocks) {
+  hipLaunchKernelGGL(k_sort_pairs, dim3(1), dim3(1024), 0, st, idx, npairs, E, offsets, sorted, blocks);
   return check_launch("sort pairs by expert");
 }
 
@@ -295,7 +374,8 @@ int launch_row_group_sums(hipStream_t st, const uint16_t* a, int64_t lda, int ro
 static size_t al(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
 size_t grouped_ws_bytes(int64_t n_pairs, int E, int x_rows, int K, int gs) {
-  return al(static_cast<size_t>(E + 1) * 4) + al(static_cast<size_t>(n_pairs) * 4) +
+  return al(static_cast<size_t>(E + 2) * 4) + al(static_cast<size_t>(n_pairs) * 4) +
+         al(static_cast<size_t>(grouped_max_blocks(static_cast<int>(n_pairs), E)) * 4) +
          al(static_cast<size_t>(x_rows) * (K / gs) * 4);
 }
 
@@ -338,9 +418,11 @@ extern "C" int zmoe_grouped_gather_qmm(void* stream, const void* x, int64_t x_ba
   hipStream_t st = as_stream(stream);
   char* base = static_cast<char*>(workspace);
   int* offsets = reinterpret_cast<int*>(base);
-  int* sorted = reinterpret_cast<int*>(base + al(static_cast<size_t>(E + 1) * 4));
-  float* asum = reinterpret_cast<float*>(base + al(static_cast<size_t>(E + 1) * 4) + al(static_cast<size_t>(n_pairs) * 4));
-  int rc = launch_sort_pairs(st, rhs_indices, static_cast<int>(n_pairs), E, offsets, sorted);
+  int* sorted = reinterpret_cast<int*>(base + al(static_cast<size_t>(E + 2) * 4));
+  int* blocks = reinterpret_cast<int*>(base + al(static_cast<size_t>(E + 2) * 4) + al(static_cast<size_t>(n_pairs) * 4));
+  float* asum = reinterpret_cast<float*>(
+      reinterpret_cast<char*>(blocks) + al(static_cast<size_t>(grouped_max_blocks(static_cast<int>(n_pairs), E)) * 4));
+  int rc = launch_sort_pairs(st, rhs_indices, static_cast<int>(n_pairs), E, offsets, sorted, blocks);
   if (rc) return rc;
   if (quant_mode == ZMOE_Q_AFFINE) {
     rc = launch_row_group_sums(st, static_cast<const uint16_t*>(x), K, static_cast<int>(x_batch), K, group_size, asum);
@@ -351,6 +433,8 @@ extern "C" int zmoe_grouped_gather_qmm(void* stream, const void* x, int64_t x_ba
   g.lda = K;
   g.asum = asum;
   g.offsets = offsets;
+  g.blocks = blocks;
+  g.E = E;
   g.sorted = sorted;
   g.lhs = lhs_indices;
   g.a_div = 0;

@@ -43,6 +43,7 @@ struct LayerWs {
   void* sh_y;     // [B, H] bf16
   int* offsets;   // grouped path: [E+1] pair ranges by expert
   int* sorted;    //   [B*K] pairs in expert order
+  int* blocks;    //   32-row blocks of every expert
   float* xsum;    //   affine: [B][H/gs] group sums of x
   float* asum;    //   affine: [B*K][I/gs] group sums of act
   size_t bytes;
@@ -66,8 +67,9 @@ static LayerWs layout_ws(const zmoe_layer_desc* d, int B, char* base) {
   ws.sh_y = take(static_cast<size_t>(B) * (d->shared_inter > 0 ? d->hidden : 0) * 2);
   if (use_grouped(d, B)) {
     const int gs = d->group_size > 0 ? d->group_size : 32;
-    ws.offsets = static_cast<int*>(take(static_cast<size_t>(d->n_experts + 1) * 4));
+    ws.offsets = static_cast<int*>(take(static_cast<size_t>(d->n_experts + 2) * 4));
     ws.sorted = static_cast<int*>(take(BK * 4));
+    ws.blocks = static_cast<int*>(take(static_cast<size_t>(grouped_max_blocks(static_cast<int>(BK), d->n_experts)) * 4));
     ws.xsum = static_cast<float*>(take(static_cast<size_t>(B) * (d->hidden / gs) * 4));
     ws.asum = static_cast<float*>(take(BK * (d->inter / gs) * 4));
   }
@@ -190,7 +192,7 @@ extern "C" int zmoe_moe_layer(void* stream, const zmoe_layer_desc* d, const void
     // and y stay in pair order
     const int npairs = B * K;
     const bool affine = d->quant_mode == ZMOE_Q_AFFINE;
-    rc = launch_sort_pairs(st, ws.idx, npairs, E, ws.offsets, ws.sorted);
+    rc = launch_sort_pairs(st, ws.idx, npairs, E, ws.offsets, ws.sorted, ws.blocks);
     if (rc) return rc;
     if (affine) {
       rc = launch_row_group_sums(st, static_cast<const uint16_t*>(x), H, B, H, d->group_size, ws.xsum);
@@ -201,6 +203,8 @@ extern "C" int zmoe_moe_layer(void* stream, const zmoe_layer_desc* d, const void
     g.lda = H;
     g.asum = ws.xsum;
     g.offsets = ws.offsets;
+    g.blocks = ws.blocks;
+    g.E = E;
     g.sorted = ws.sorted;
     g.lhs = nullptr;
     g.a_div = K;  // pair (b, k) reads token b
