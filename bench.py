@@ -41,7 +41,7 @@ HBM_PEAK_GBPS = 8000.0
 H, E, K, I, GS = 2048, 128, 8, 768, 64
 LAYERS = 48
 ROOT = Path(__file__).resolve().parent
-TRAFFIC_FILE = ROOT / "profiles" / "k_moe_decode_qwen3_b1_traffic.json"
+TRAFFIC_FILE = ROOT / "profiles" / "k_moe_decode1_qwen3_b1_traffic.json"
 COPY_BYTES = 256 << 20  # calibration copy of --profile-run: reads and writes this many bytes
 
 
