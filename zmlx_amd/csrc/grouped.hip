@@ -5,9 +5,13 @@
 // of mlx_lm's SwitchGLU sort path + gather_qmm(sorted_indices=True) that the
 // reference keeps for M > 1, moe_mlp.py:540-543).
 //
-// Tiles: a workgroup of 4 waves owns (expert e, 128 output rows n); wave w
-// computes n0 = 128*tile + 32*w .. +31 for every 32-row block of the
-// expert's sorted rows, with v_mfma_f32_32x32x16_bf16.
+// Tiles: a workgroup of 8 waves owns (expert e, a chunk of up to 64 of its
+// sorted rows, 256 output rows n); wave w computes n0 = 256*tile + 32*w .. +31
+// for both 32-row blocks of the chunk with v_mfma_f32_32x32x16_bf16, so each
+// weight load feeds two blocks.  Per 64-k block the chunk's activations are
+// loaded once by the whole workgroup into LDS (one 16-byte load per thread,
+// double-buffered) and read from there by every wave.  Chunks come from the
+// sort kernel's list, so a heavy expert spreads over many workgroups.
 //
 // In-register dequant keeps the decode GEMV's exact products: the weight
 // operand is the bf16 number 128+q (q = the 4-bit code, exact in bf16, made
@@ -38,9 +42,13 @@ namespace zmoe {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-constexpr int kGThreads = 256;  // 4 waves
-constexpr int kGTileN = 128;    // output rows per workgroup
-constexpr int kGTileM = 32;     // sorted rows per MFMA block
+constexpr int kGThreads = 512;  // 8 waves
+constexpr int kGWaves = kGThreads / 64;
+constexpr int kGTileN = 32 * kGWaves;  // output rows per workgroup
+constexpr int kGTileM = 32;            // sorted rows per MFMA block
+constexpr int kGBlocksM = 2;           // MFMA blocks per chunk
+constexpr int kGChunk = kGTileM * kGBlocksM;
+constexpr int kGLdsRow = 64 + 8;       // bf16 per staged activation row (64 k + pad)
 
 
 // ---------------------------------------------------------------------------
@@ -66,18 +74,19 @@ __global__ __launch_bounds__(1024) void k_sort_pairs(const uint32_t* __restrict_
   __syncthreads();
   for (int e = threadIdx.x; e <= E; e += blockDim.x) offsets[e] = off[e];
   if (blocks) {
-    // 32-row blocks of every expert, in expert order (their starts reuse cnt)
+    // chunks of kGChunk rows of every expert, in expert order (their starts
+    // reuse cnt)
     if (threadIdx.x == 0) {
       int nb = 0;
       for (int e = 0; e < E; ++e) {
         cnt[e] = nb;
-        nb += (off[e + 1] - off[e] + 31) / 32;
+        nb += (off[e + 1] - off[e] + kGChunk - 1) / kGChunk;
       }
       offsets[E + 1] = nb;
     }
     __syncthreads();
     for (int e = threadIdx.x; e < E; e += blockDim.x) {
-      const int nbe = (off[e + 1] - off[e] + 31) / 32;
+      const int nbe = (off[e + 1] - off[e] + kGChunk - 1) / kGChunk;
       for (int j = 0; j < nbe; ++j) blocks[cnt[e] + j] = e | (j << 11);
     }
     __syncthreads();
@@ -154,177 +163,272 @@ __device__ __forceinline__ float group_scale(const void* s, int64_t i) {
 // ---------------------------------------------------------------------------
 // the grouped GEMM
 // ---------------------------------------------------------------------------
-template <int QMODE, bool G32, bool SWIGLU>
+// Bytes of the LDS parameter cache (0 if it does not fit): per wave its 32
+// rows' scales (and biases) of every group, then (affine) the chunk rows'
+// group sums of the activations.
+__host__ __device__ inline size_t grouped_pcache_bytes(int qmode, bool swiglu, int G) {
+  const size_t per_row = (qmode == ZMOE_Q_AFFINE) ? static_cast<size_t>(G) * 2 * 2 : static_cast<size_t>(G);
+  const size_t arrays = swiglu ? 2 : 1;
+  size_t bytes = static_cast<size_t>(kGWaves) * 32 * per_row * arrays;
+  bytes = (bytes + 15) & ~static_cast<size_t>(15);
+  if (qmode == ZMOE_Q_AFFINE) bytes += static_cast<size_t>(kGChunk) * G * 4;
+  return bytes;
+}
+constexpr size_t kGPcacheMax = 96 * 1024;
+
+template <int QMODE, int GS, bool SWIGLU, bool PLDS>
 __global__ __launch_bounds__(kGThreads) void k_grouped_qmm(GroupedArgs g) {
+  __shared__ __align__(16) uint16_t alds[2][kGChunk * kGLdsRow];
+  extern __shared__ __align__(16) unsigned char pcache[];
+  constexpr bool G32 = GS == 32;
+  constexpr int KPG = GS / 16;  // k-steps per quantisation group
+  constexpr int PB = (QMODE == ZMOE_Q_AFFINE) ? 2 : 1;  // parameter bytes
   const int ntiles = (g.N + kGTileN - 1) / kGTileN;
   const int wave = threadIdx.x / kWave;
   const int lane = __lane_id();
   const int h = lane >> 5, col = lane & 31;
-  // workgroup -> (expert, 32-row blocks, 128-row output tile): one block per
-  // workgroup from the block list (heavy experts spread over many
-  // workgroups), else every block of expert blockIdx / ntiles
-  int e, tile, m_first, m_last;
-  if (g.blocks) {
-    const int b = blockIdx.x / ntiles;
-    tile = blockIdx.x - b * ntiles;
-    if (b >= g.offsets[g.E + 1]) return;
-    const int be = g.blocks[b];
-    e = be & 2047;
-    m_first = g.offsets[e] + (be >> 11) * kGTileM;
-    m_last = min(m_first + kGTileM, g.offsets[e + 1]);
-  } else {
-    e = blockIdx.x / ntiles;
-    tile = blockIdx.x - e * ntiles;
-    m_first = g.offsets ? g.offsets[e] : 0;
-    m_last = g.offsets ? g.offsets[e + 1] : g.M;
-  }
+  const int c = blockIdx.x / ntiles;
+  const int tile = blockIdx.x - c * ntiles;
+  if (c >= g.offsets[g.E + 1]) return;  // whole workgroup: past the chunk list
+  const int ce = g.blocks[c];
+  const int e = ce & 2047;
+  const int r_begin = g.offsets[e] + (ce >> 11) * kGChunk;
+  const int r_end = min(r_begin + kGChunk, g.offsets[e + 1]);
   const int n0 = tile * kGTileN + wave * 32;
-  if (n0 >= g.N) return;
-  const int r_begin = m_first, r_end = g.offsets ? (g.blocks ? m_last : g.offsets[e + 1]) : g.M;
-  if (r_begin >= r_end) return;
+  const bool active = n0 < g.N;  // idle waves still take part in the barriers
 
   const AffineK ak = affine_k();
   const int K = g.K;
   const int nblk = K >> 6;  // 64-k blocks
-  const int G = K / g.gs;
-  const int kpg = g.gs >> 4;  // k-steps per quantisation group
+  const int G = K / GS;
   const int64_t wpr = K >> 3;
-  const int n = n0 + col;  // this lane's output row (B-operand column)
+  const int nb = min(n0, g.N - 32);  // this wave's first row (clamped for idle waves)
+  const int n = nb + col;            // this lane's output row (B-operand column)
   const int64_t erow = static_cast<int64_t>(e) * g.N + n;
   const uint32_t* W0 = g.w0 + erow * wpr;
   const uint32_t* W1 = SWIGLU ? g.w1 + erow * wpr : nullptr;
   const int64_t prow = erow * G;  // scale/bias row
 
-  for (int m0 = r_begin; m0 < r_end; m0 += kGTileM) {
-    // this lane's A row (operand row = col) and its source row
-    const int r_lane = min(m0 + col, r_end - 1);
-    const int src = g.sorted ? g.sorted[r_lane] : r_lane;
-    const int64_t arow = g.lhs ? static_cast<int64_t>(g.lhs[src])
-                                : (g.a_div > 0 ? static_cast<int64_t>(src / g.a_div) : static_cast<int64_t>(r_lane));
-    const uint16_t* A = g.a + arow * g.lda;
+  // activation row of sorted row r (clamped to the chunk)
+  auto act_row = [&](int r) -> int64_t {
+    const int rr = min(r, r_end - 1);
+    const int src = g.sorted ? g.sorted[rr] : rr;
+    return g.lhs ? static_cast<int64_t>(g.lhs[src]) : (g.a_div > 0 ? static_cast<int64_t>(src / g.a_div) : rr);
+  };
+  // cooperative staging: thread t moves 16 bytes (8 k) of row t / 8
+  const int st_row = threadIdx.x >> 3, st_q = threadIdx.x & 7;
+  const uint16_t* st_src = g.a + act_row(r_begin + st_row) * g.lda + st_q * 8;
 
-    f32x16_t tot0 = {}, tot1 = {};
-    f32x16_t acc0 = {}, acc1 = {};
-    int ks = 0;  // k-steps into the current group
-    int grp = 0;
-    const float* as_row = (QMODE == ZMOE_Q_AFFINE) ? g.asum + arow * G : nullptr;
-    // Per 64-k block: weights, activations, the scales of the groups this
-    // block completes (gs 32: two, 64: one, 128: one every other block) and
-    // the operands of one affine-offset step (two groups per f32 MFMA,
-    // G / 2 <= blocks), all loaded one block ahead of their use.
-    struct KBuf {
-      uint32_t w0[4], w1[4];
-      uint4 av[4];
-      uint32_t s0[2], s1[2];  // raw scales
-      float xs;               // offset step: group sum of a
-      uint32_t os0, ob0, os1, ob1;  // offset step: raw scale / bias
-    };
-    const int gpb2 = 128 / g.gs;  // groups completed per 2 blocks
-    const int nsteps = G >> 1;
-    auto raw_scale = [&](const void* sp, int64_t i) -> uint32_t {
-      if (QMODE == ZMOE_Q_AFFINE) return gload(static_cast<const uint16_t*>(sp) + i);
-      return gload(static_cast<const uint8_t*>(sp) + i);
-    };
-    auto load_blk = [&](int blk, KBuf& kb) {
-      if (!G32) {
-        const uint4 q0 = gload(reinterpret_cast<const uint4*>(W0 + blk * 8 + h * 4));
-        kb.w0[0] = q0.x, kb.w0[1] = q0.y, kb.w0[2] = q0.z, kb.w0[3] = q0.w;
-        if (SWIGLU) {
-          const uint4 q1 = gload(reinterpret_cast<const uint4*>(W1 + blk * 8 + h * 4));
-          kb.w1[0] = q1.x, kb.w1[1] = q1.y, kb.w1[2] = q1.z, kb.w1[3] = q1.w;
-        }
+  // ---- parameter cache (PLDS): this wave's rows' scales/biases, chunk sums
+  const size_t row_bytes = static_cast<size_t>(G) * PB;
+  const size_t wave_bytes = 32 * row_bytes * (QMODE == ZMOE_Q_AFFINE ? 2 : 1);
+  unsigned char* pw = pcache + wave * wave_bytes * (SWIGLU ? 2 : 1);  // [matrix][s, b][32 rows][G]
+  float* pxs = reinterpret_cast<float*>(
+      pcache + ((static_cast<size_t>(kGWaves) * wave_bytes * (SWIGLU ? 2 : 1) + 15) & ~static_cast<size_t>(15)));
+  if (PLDS) {
+    // each array of the wave's 32 rows is one contiguous block of 32 * G params
+    const int64_t base_el = (static_cast<int64_t>(e) * g.N + nb) * G;
+    const int nvec = static_cast<int>((32 * row_bytes) >> 4);  // 16-byte pieces per array
+    const void* srcs[4] = {g.s0, (QMODE == ZMOE_Q_AFFINE) ? g.b0 : nullptr, g.s1, (QMODE == ZMOE_Q_AFFINE) ? g.b1 : nullptr};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) kb.av[j] = gload(reinterpret_cast<const uint4*>(A + blk * 64 + h * 32 + j * 8));
-      } else {
-        const uint4 qa = gload(reinterpret_cast<const uint4*>(W0 + blk * 8));
-        const uint4 qb = gload(reinterpret_cast<const uint4*>(W0 + blk * 8 + 4));
-        kb.w0[0] = h ? qa.y : qa.x, kb.w0[1] = h ? qa.w : qa.z, kb.w0[2] = h ? qb.y : qb.x, kb.w0[3] = h ? qb.w : qb.z;
-        if (SWIGLU) {
-          const uint4 ua = gload(reinterpret_cast<const uint4*>(W1 + blk * 8));
-          const uint4 ub = gload(reinterpret_cast<const uint4*>(W1 + blk * 8 + 4));
-          kb.w1[0] = h ? ua.y : ua.x, kb.w1[1] = h ? ua.w : ua.z, kb.w1[2] = h ? ub.y : ub.x,
-          kb.w1[3] = h ? ub.w : ub.z;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) kb.av[j] = gload(reinterpret_cast<const uint4*>(A + blk * 64 + (2 * j + h) * 8));
-      }
-      // groups completed in this block: [first, first + cnt)
-      const int first = (blk * gpb2) >> 1;
-      const int cnt = (((blk + 1) * gpb2) >> 1) - first;
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int gi = min(first + i, G - 1);
-        kb.s0[i] = i < cnt ? raw_scale(g.s0, prow + gi) : 0u;
-        if (SWIGLU) kb.s1[i] = i < cnt ? raw_scale(g.s1, prow + gi) : 0u;
-      }
-      if (QMODE == ZMOE_Q_AFFINE) {
-        const int gi = min(2 * blk + h, G - 1);
-        const bool ok = blk < nsteps && 2 * blk + h < G;
-        kb.xs = ok ? as_row[gi] : 0.0f;
-        kb.os0 = ok ? gload(static_cast<const uint16_t*>(g.s0) + prow + gi) : 0u;
-        kb.ob0 = ok ? gload(static_cast<const uint16_t*>(g.b0) + prow + gi) : 0u;
-        if (SWIGLU) {
-          kb.os1 = ok ? gload(static_cast<const uint16_t*>(g.s1) + prow + gi) : 0u;
-          kb.ob1 = ok ? gload(static_cast<const uint16_t*>(g.b1) + prow + gi) : 0u;
-        }
-      }
-    };
-    auto decode_scale = [&](uint32_t r) -> float {
-      if (QMODE == ZMOE_Q_AFFINE) return bf16_bits_to_f32(r);
-      return e8m0_to_f32(r);
-    };
-    auto compute_blk = [&](int blk, const KBuf& kb) {
-      int done = 0;  // groups completed so far in this block
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const bf16x8_t xa = (QMODE == ZMOE_Q_AFFINE) ? act_affine(kb.av[j]) : act_natural(kb.av[j]);
-        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa, wt_operand<QMODE>(kb.w0[j], ak), acc0, 0, 0, 0);
-        if (SWIGLU) acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa, wt_operand<QMODE>(kb.w1[j], ak), acc1, 0, 0, 0);
-        if (++ks == kpg) {  // group complete: scale into the totals
-          ks = 0;
-          const float s0 = decode_scale(done == 0 ? kb.s0[0] : kb.s0[1]);
-          const float s1 = SWIGLU ? decode_scale(done == 0 ? kb.s1[0] : kb.s1[1]) : 0.0f;
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            tot0[i] = fmaf(s0, acc0[i], tot0[i]);
-            acc0[i] = 0.0f;
-            if (SWIGLU) {
-              tot1[i] = fmaf(s1, acc1[i], tot1[i]);
-              acc1[i] = 0.0f;
-            }
-          }
-          ++grp;
-          ++done;
-        }
-      }
-      if (QMODE == ZMOE_Q_AFFINE && blk < nsteps) {
-        // + (b_g - 128 s_g) * asum_g for groups 2 blk, 2 blk + 1
-        const float c0 = bf16_bits_to_f32(kb.ob0) - 128.0f * bf16_bits_to_f32(kb.os0);
-        tot0 = __builtin_amdgcn_mfma_f32_32x32x2f32(kb.xs, c0, tot0, 0, 0, 0);
-        if (SWIGLU) {
-          const float c1 = bf16_bits_to_f32(kb.ob1) - 128.0f * bf16_bits_to_f32(kb.os1);
-          tot1 = __builtin_amdgcn_mfma_f32_32x32x2f32(kb.xs, c1, tot1, 0, 0, 0);
-        }
-      }
-    };
-    // next block's loads in flight while the current one runs on MFMA
-    KBuf kb0, kb1;
-    load_blk(0, kb0);
-    for (int blk = 0; blk < nblk; blk += 2) {
-      if (blk + 1 < nblk) load_blk(blk + 1, kb1);
-      compute_blk(blk, kb0);
-      if (blk + 1 < nblk) {
-        if (blk + 2 < nblk) load_blk(blk + 2, kb0);
-        compute_blk(blk + 1, kb1);
+    for (int m = 0; m < 4; ++m) {
+      const bool use = (m < 2 || SWIGLU) && (QMODE == ZMOE_Q_AFFINE || (m & 1) == 0);
+      if (!use) continue;
+      const int slot = (QMODE == ZMOE_Q_AFFINE) ? m : (m >> 1);
+      const uint4* src = reinterpret_cast<const uint4*>(static_cast<const unsigned char*>(srcs[m]) + base_el * PB);
+      uint4* dst = reinterpret_cast<uint4*>(pw + slot * 32 * row_bytes);
+      for (int i = lane; i < nvec; i += kWave) dst[i] = gload(src + i);
+    }
+    if (QMODE == ZMOE_Q_AFFINE) {
+      // chunk rows' group sums (G floats per row)
+      for (int i = threadIdx.x; i < kGChunk * G; i += kGThreads) {
+        const int r = i / G, q = i - r * G;
+        pxs[i] = gload(g.asum + act_row(r_begin + r) * G + q);
       }
     }
-    // epilogue: element i is row (i/4)*8 + h*4 + i%4 of the block, column n
+  }
+  auto pscale = [&](int m, int gi) -> float {  // scale of this lane's row, matrix m, group gi
+    if (QMODE == ZMOE_Q_AFFINE) {
+      const uint16_t* a = reinterpret_cast<const uint16_t*>(pw + (m * 2) * 32 * row_bytes);
+      return bf16_bits_to_f32(a[col * G + gi]);
+    }
+    return e8m0_to_f32(pw[m * 32 * row_bytes + col * G + gi]);
+  };
+  auto poffset = [&](int m, int gi) -> float {  // affine: b - 128 s
+    const uint16_t* sa = reinterpret_cast<const uint16_t*>(pw + (m * 2) * 32 * row_bytes);
+    const uint16_t* ba = reinterpret_cast<const uint16_t*>(pw + (m * 2 + 1) * 32 * row_bytes);
+    return bf16_bits_to_f32(ba[col * G + gi]) - 128.0f * bf16_bits_to_f32(sa[col * G + gi]);
+  };
+  // this lane's rows in the two MFMA blocks (affine offset operand, no cache)
+  const float* as_row[kGBlocksM];
+#pragma unroll
+  for (int mb = 0; mb < kGBlocksM; ++mb)
+    as_row[mb] = (QMODE == ZMOE_Q_AFFINE && !PLDS) ? g.asum + act_row(r_begin + mb * kGTileM + col) * G : nullptr;
+
+  f32x16_t tot0[kGBlocksM], tot1[kGBlocksM], acc0[kGBlocksM], acc1[kGBlocksM];
+#pragma unroll
+  for (int mb = 0; mb < kGBlocksM; ++mb) tot0[mb] = tot1[mb] = acc0[mb] = acc1[mb] = f32x16_t{};
+  const int nsteps = G >> 1;
+  constexpr int kGpb2 = 128 / GS;  // groups completed per 2 blocks
+  // Per 64-k block, one block ahead of use: this lane's weights, this
+  // thread's 16 staged activation bytes, and without the cache the scales of
+  // the groups the block completes and one affine-offset step's operands.
+  struct KBuf {
+    uint32_t w0[4], w1[4];
+    uint32_t s0[2], s1[2];
+    float xs[kGBlocksM];
+    uint32_t os0, ob0, os1, ob1;
+    uint4 st;
+  };
+  auto raw_scale = [&](const void* sp, int64_t i) -> uint32_t {
+    if (QMODE == ZMOE_Q_AFFINE) return gload(static_cast<const uint16_t*>(sp) + i);
+    return gload(static_cast<const uint8_t*>(sp) + i);
+  };
+  auto load_blk = [&](int blk, KBuf& kb) {
+    kb.st = gload(reinterpret_cast<const uint4*>(st_src + blk * 64));
+    if (!G32) {
+      const uint4 q0 = gload(reinterpret_cast<const uint4*>(W0 + blk * 8 + h * 4));
+      kb.w0[0] = q0.x, kb.w0[1] = q0.y, kb.w0[2] = q0.z, kb.w0[3] = q0.w;
+      if (SWIGLU) {
+        const uint4 q1 = gload(reinterpret_cast<const uint4*>(W1 + blk * 8 + h * 4));
+        kb.w1[0] = q1.x, kb.w1[1] = q1.y, kb.w1[2] = q1.z, kb.w1[3] = q1.w;
+      }
+    } else {
+      const uint4 qa = gload(reinterpret_cast<const uint4*>(W0 + blk * 8));
+      const uint4 qb = gload(reinterpret_cast<const uint4*>(W0 + blk * 8 + 4));
+      kb.w0[0] = h ? qa.y : qa.x, kb.w0[1] = h ? qa.w : qa.z, kb.w0[2] = h ? qb.y : qb.x, kb.w0[3] = h ? qb.w : qb.z;
+      if (SWIGLU) {
+        const uint4 ua = gload(reinterpret_cast<const uint4*>(W1 + blk * 8));
+        const uint4 ub = gload(reinterpret_cast<const uint4*>(W1 + blk * 8 + 4));
+        kb.w1[0] = h ? ua.y : ua.x, kb.w1[1] = h ? ua.w : ua.z, kb.w1[2] = h ? ub.y : ub.x, kb.w1[3] = h ? ub.w : ub.z;
+      }
+    }
+    if (PLDS) return;
+    const int first = (blk * kGpb2) >> 1;
+    const int cnt = (((blk + 1) * kGpb2) >> 1) - first;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int gi = min(first + i, G - 1);
+      kb.s0[i] = i < cnt ? raw_scale(g.s0, prow + gi) : 0u;
+      if (SWIGLU) kb.s1[i] = i < cnt ? raw_scale(g.s1, prow + gi) : 0u;
+    }
+    if (QMODE == ZMOE_Q_AFFINE) {
+      const int gi = min(2 * blk + h, G - 1);
+      const bool ok = blk < nsteps && 2 * blk + h < G;
+#pragma unroll
+      for (int mb = 0; mb < kGBlocksM; ++mb) kb.xs[mb] = ok ? as_row[mb][gi] : 0.0f;
+      kb.os0 = ok ? gload(static_cast<const uint16_t*>(g.s0) + prow + gi) : 0u;
+      kb.ob0 = ok ? gload(static_cast<const uint16_t*>(g.b0) + prow + gi) : 0u;
+      if (SWIGLU) {
+        kb.os1 = ok ? gload(static_cast<const uint16_t*>(g.s1) + prow + gi) : 0u;
+        kb.ob1 = ok ? gload(static_cast<const uint16_t*>(g.b1) + prow + gi) : 0u;
+      }
+    }
+  };
+  // staged activations are stored already in the operand order: affine pairs
+  // (x0,x4) (x1,x5) (x2,x6) (x3,x7)
+  auto stage = [&](const KBuf& kb, int buf) {
+    uint4 v = kb.st;
+    if (QMODE == ZMOE_Q_AFFINE) v = __builtin_bit_cast(uint4, act_affine(v));
+    *reinterpret_cast<uint4*>(&alds[buf][st_row * kGLdsRow + st_q * 8]) = v;
+  };
+  auto decode_scale = [&](uint32_t r) -> float {
+    if (QMODE == ZMOE_Q_AFFINE) return bf16_bits_to_f32(r);
+    return e8m0_to_f32(r);
+  };
+  auto compute_blk = [&](int blk, const KBuf& kb, int buf) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bf16x8_t b0 = wt_operand<QMODE>(kb.w0[j], ak);
+      const bf16x8_t b1 = SWIGLU ? wt_operand<QMODE>(kb.w1[j], ak) : b0;
+      const int koff = G32 ? (2 * j + h) * 8 : h * 32 + j * 8;
+      // first k-step of a group starts from a zero accumulator
+      const bool fresh = ((blk * 4 + j) % KPG) == 0;
+#pragma unroll
+      for (int mb = 0; mb < kGBlocksM; ++mb) {
+        const uint4 av = *reinterpret_cast<const uint4*>(&alds[buf][(mb * kGTileM + col) * kGLdsRow + koff]);
+        const bf16x8_t xa = act_natural(av);
+        acc0[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa, b0, fresh ? f32x16_t{} : acc0[mb], 0, 0, 0);
+        if (SWIGLU)
+          acc1[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa, b1, fresh ? f32x16_t{} : acc1[mb], 0, 0, 0);
+      }
+      if (((blk * 4 + j + 1) % KPG) == 0) {  // group complete: scale into the totals
+        const int gi = (blk * 4 + j) / KPG;
+        float s0, s1 = 0.0f;
+        if (PLDS) {
+          s0 = pscale(0, gi);
+          if (SWIGLU) s1 = pscale(1, gi);
+        } else {
+          const int done = gi - ((blk * kGpb2) >> 1);
+          s0 = decode_scale(done == 0 ? kb.s0[0] : kb.s0[1]);
+          if (SWIGLU) s1 = decode_scale(done == 0 ? kb.s1[0] : kb.s1[1]);
+        }
+#pragma unroll
+        for (int mb = 0; mb < kGBlocksM; ++mb) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            tot0[mb][i] = fmaf(s0, acc0[mb][i], tot0[mb][i]);
+            if (SWIGLU) tot1[mb][i] = fmaf(s1, acc1[mb][i], tot1[mb][i]);
+          }
+        }
+      }
+    }
+    if (QMODE == ZMOE_Q_AFFINE && blk < nsteps) {
+      // + (b_g - 128 s_g) * asum_g for groups 2 blk, 2 blk + 1
+      const int gi = min(2 * blk + h, G - 1);
+      const bool ok = 2 * blk + h < G;
+      float c0, c1 = 0.0f, xs[kGBlocksM];
+      if (PLDS) {
+        c0 = ok ? poffset(0, gi) : 0.0f;
+        if (SWIGLU) c1 = ok ? poffset(1, gi) : 0.0f;
+#pragma unroll
+        for (int mb = 0; mb < kGBlocksM; ++mb) xs[mb] = ok ? pxs[(mb * kGTileM + col) * G + gi] : 0.0f;
+      } else {
+        c0 = bf16_bits_to_f32(kb.ob0) - 128.0f * bf16_bits_to_f32(kb.os0);
+        if (SWIGLU) c1 = bf16_bits_to_f32(kb.ob1) - 128.0f * bf16_bits_to_f32(kb.os1);
+#pragma unroll
+        for (int mb = 0; mb < kGBlocksM; ++mb) xs[mb] = kb.xs[mb];
+      }
+#pragma unroll
+      for (int mb = 0; mb < kGBlocksM; ++mb) {
+        tot0[mb] = __builtin_amdgcn_mfma_f32_32x32x2f32(xs[mb], c0, tot0[mb], 0, 0, 0);
+        if (SWIGLU) tot1[mb] = __builtin_amdgcn_mfma_f32_32x32x2f32(xs[mb], c1, tot1[mb], 0, 0, 0);
+      }
+    }
+  };
+
+  // three blocks of loads in flight: block s computes from LDS buffer s % 2
+  // while block s + 1 is staged into the other and block s + 2 loads
+  KBuf kb[3];
+  load_blk(0, kb[0]);
+  if (nblk > 1) load_blk(1, kb[1]);
+  stage(kb[0], 0);
+  __syncthreads();
+  auto step = [&](int s, KBuf& cur, KBuf& nxt, KBuf& nxt2) {
+    if (s + 2 < nblk) load_blk(s + 2, nxt2);
+    if (active) compute_blk(s, cur, s & 1);
+    if (s + 1 < nblk) {
+      stage(nxt, (s + 1) & 1);
+      __syncthreads();
+    }
+  };
+  for (int blk = 0; blk < nblk; blk += 3) {
+    step(blk, kb[0], kb[1], kb[2]);
+    if (blk + 1 < nblk) step(blk + 1, kb[1], kb[2], kb[0]);
+    if (blk + 2 < nblk) step(blk + 2, kb[2], kb[0], kb[1]);
+  }
+  if (!active) return;
+  // epilogue: element i of block mb is row mb*32 + (i/4)*8 + h*4 + i%4 of
+  // the chunk, column n
+#pragma unroll
+  for (int mb = 0; mb < kGBlocksM; ++mb) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int r = m0 + (i >> 2) * 8 + h * 4 + (i & 3);
+      const int r = r_begin + mb * kGTileM + (i >> 2) * 8 + h * 4 + (i & 3);
       if (r < r_end) {
         const int64_t orow = g.scatter ? static_cast<int64_t>(g.sorted[r]) : static_cast<int64_t>(r);
-        const uint32_t v = SWIGLU ? swiglu_bf16(round_bf16(tot0[i]), round_bf16(tot1[i])) : f32_to_bf16_bits(tot0[i]);
+        const uint32_t v =
+            SWIGLU ? swiglu_bf16(round_bf16(tot0[mb][i]), round_bf16(tot1[mb][i])) : f32_to_bf16_bits(tot0[mb][i]);
         g.out[orow * g.ldo + n] = static_cast<uint16_t>(v);
       }
     }
@@ -334,25 +438,42 @@ __global__ __launch_bounds__(kGThreads) void k_grouped_qmm(GroupedArgs g) {
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
-template <int QMODE, bool G32, bool SWIGLU>
+template <int QMODE, int GS, bool SWIGLU>
 static void launch_grouped_t(hipStream_t st, const GroupedArgs& g, int n_experts) {
   const int ntiles = (g.N + kGTileN - 1) / kGTileN;
-  const int units = g.blocks ? grouped_max_blocks(g.M, n_experts) : n_experts;
-  hipLaunchKernelGGL((k_grouped_qmm<QMODE, G32, SWIGLU>), dim3(units * ntiles), dim3(kGThreads), 0, st, g);
+  const int units = grouped_max_blocks(g.M, n_experts);
+  const size_t pc = grouped_pcache_bytes(QMODE, SWIGLU, g.K / GS);
+  if (pc <= kGPcacheMax) {
+    static bool prepared = false;
+    if (!prepared) {
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_grouped_qmm<QMODE, GS, SWIGLU, true>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kGPcacheMax));
+      prepared = true;
+    }
+    hipLaunchKernelGGL((k_grouped_qmm<QMODE, GS, SWIGLU, true>), dim3(units * ntiles), dim3(kGThreads), pc, st, g);
+  } else {
+    hipLaunchKernelGGL((k_grouped_qmm<QMODE, GS, SWIGLU, false>), dim3(units * ntiles), dim3(kGThreads), 0, st, g);
+  }
 }
 
 int launch_grouped(hipStream_t st, const GroupedArgs& g, int n_experts, int quant_mode, bool swiglu) {
-  const bool g32 = g.gs == 32;
   if (quant_mode == ZMOE_Q_AFFINE) {
-    if (g32)
-      swiglu ? launch_grouped_t<ZMOE_Q_AFFINE, true, true>(st, g, n_experts)
-             : launch_grouped_t<ZMOE_Q_AFFINE, true, false>(st, g, n_experts);
-    else
-      swiglu ? launch_grouped_t<ZMOE_Q_AFFINE, false, true>(st, g, n_experts)
-             : launch_grouped_t<ZMOE_Q_AFFINE, false, false>(st, g, n_experts);
+    switch (g.gs) {
+      case 32:
+        swiglu ? launch_grouped_t<ZMOE_Q_AFFINE, 32, true>(st, g, n_experts)
+               : launch_grouped_t<ZMOE_Q_AFFINE, 32, false>(st, g, n_experts);
+        break;
+      case 128:
+        swiglu ? launch_grouped_t<ZMOE_Q_AFFINE, 128, true>(st, g, n_experts)
+               : launch_grouped_t<ZMOE_Q_AFFINE, 128, false>(st, g, n_experts);
+        break;
+      default:
+        swiglu ? launch_grouped_t<ZMOE_Q_AFFINE, 64, true>(st, g, n_experts)
+               : launch_grouped_t<ZMOE_Q_AFFINE, 64, false>(st, g, n_experts);
+    }
   } else {
-    swiglu ? launch_grouped_t<ZMOE_Q_MXFP4, true, true>(st, g, n_experts)
-           : launch_grouped_t<ZMOE_Q_MXFP4, true, false>(st, g, n_experts);
+    swiglu ? launch_grouped_t<ZMOE_Q_MXFP4, 32, true>(st, g, n_experts)
+           : launch_grouped_t<ZMOE_Q_MXFP4, 32, false>(st, g, n_experts);
   }
   return check_launch("grouped gather_qmm");
 }

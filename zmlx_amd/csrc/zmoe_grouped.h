@@ -11,9 +11,8 @@ struct GroupedArgs {
   const uint16_t* a;     // activation rows (bf16)
   int64_t lda;           // elements between rows
   const float* asum;     // affine: [a rows][K/gs] group sums of a (fp32)
-  const int* offsets;    // [E+2] sorted row ranges, [E+1] = number of 32-row blocks;
-                         // nullptr: one expert, rows [0, M)
-  const int* blocks;     // [blocks] expert | (block within the expert << 11), or nullptr
+  const int* offsets;    // [E+2] sorted row ranges, [E+1] = number of row chunks
+  const int* blocks;     // [chunks] expert | (chunk within the expert << 11)
   const int* sorted;     // [rows] pair ids in expert order; nullptr: identity
   const uint32_t* lhs;   // a row = lhs[pair] when set, else pair / a_div
   int a_div;             //   (a_div > 0), else the sorted row r itself
@@ -35,10 +34,10 @@ struct GroupedArgs {
 // swiglu (w1/s1/b1 = up), else one matrix.
 int launch_grouped(hipStream_t st, const GroupedArgs& g, int n_experts, int quant_mode, bool swiglu);
 // offsets[E+2] / sorted[npairs]: the pairs (token, k) in expert order;
-// blocks[]: every expert's 32-row blocks (at most npairs / 32 + E of them).
+// blocks[]: every expert's 64-row chunks (at most npairs / 64 + E of them).
 int launch_sort_pairs(hipStream_t st, const uint32_t* idx, int npairs, int E, int* offsets, int* sorted, int* blocks);
-// Upper bound on the 32-row blocks of npairs pairs over E experts.
-inline int grouped_max_blocks(int npairs, int E) { return (npairs + 31) / 32 + E; }
+// Upper bound on the 64-row chunks of npairs pairs over E experts.
+inline int grouped_max_blocks(int npairs, int E) { return (npairs + 63) / 64 + E; }
 // out[r][g] = fp32 sum of a[r][g*gs .. +gs).
 int launch_row_group_sums(hipStream_t st, const uint16_t* a, int64_t lda, int rows, int K, int gs, float* out);
 
