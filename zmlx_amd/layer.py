@@ -94,6 +94,12 @@ class QuantizedMoELayer:
         if combine not in COMBINES:
             raise ValueError(f"unknown combine mode {combine!r}")
         self.device = router_weight.device
+        if self.device.type != "cuda":
+            raise ValueError("QuantizedMoELayer: weights must be device (GPU) tensors")
+        for p in (gate, up, down) + (tuple(shared) if shared is not None else ()):
+            for t in (p.weight, p.scales, p.biases):
+                if t is not None and t.device != self.device:
+                    raise ValueError("QuantizedMoELayer: all weights must be on the router weight's device")
         E, H = (int(s) for s in router_weight.shape)
         self.hidden, self.n_experts, self.top_k = H, E, int(top_k)
         self.inter = int(gate.weight.shape[-2])
