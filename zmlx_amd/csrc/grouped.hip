@@ -36,6 +36,7 @@
 #include "zmoe_host.h"
 
 #include <string>
+#include <type_traits>
 
 namespace zmoe {
 
@@ -49,6 +50,7 @@ constexpr int kGTileM = 32;            // sorted rows per MFMA block
 constexpr int kGBlocksM = 2;           // MFMA blocks per chunk
 constexpr int kGChunk = kGTileM * kGBlocksM;
 constexpr int kGLdsRow = 64 + 8;       // bf16 per staged activation row (64 k + pad)
+constexpr int kGStage = kGChunk * 8 / kGThreads;  // 16-byte staging pieces per thread
 
 
 // ---------------------------------------------------------------------------
@@ -176,7 +178,7 @@ __host__ __device__ inline size_t grouped_pcache_bytes(int qmode, bool swiglu, i
 }
 constexpr size_t kGPcacheMax = 96 * 1024;
 
-template <int QMODE, int GS, bool SWIGLU, bool PLDS>
+template <int QMODE, int GS, bool SWIGLU, bool PLDS, int NB>
 __global__ __launch_bounds__(kGThreads) void k_grouped_qmm(GroupedArgs g) {
   __shared__ __align__(16) uint16_t alds[2][kGChunk * kGLdsRow];
   extern __shared__ __align__(16) unsigned char pcache[];
@@ -215,14 +217,18 @@ __global__ __launch_bounds__(kGThreads) void k_grouped_qmm(GroupedArgs g) {
     const int src = g.sorted ? g.sorted[rr] : rr;
     return g.lhs ? static_cast<int64_t>(g.lhs[src]) : (g.a_div > 0 ? static_cast<int64_t>(src / g.a_div) : rr);
   };
-  // cooperative staging: thread t moves 16 bytes (8 k) of row t / 8
+  // cooperative staging: thread t moves kGStage pieces of 16 bytes (8 k),
+  // rows t / 8 + i * (threads / 8)
   const int st_row = threadIdx.x >> 3, st_q = threadIdx.x & 7;
-  const uint16_t* st_src = g.a + act_row(r_begin + st_row) * g.lda + st_q * 8;
+  const uint16_t* st_src[kGStage];
+#pragma unroll
+  for (int i = 0; i < kGStage; ++i)
+    st_src[i] = g.a + act_row(r_begin + st_row + i * (kGThreads / 8)) * g.lda + st_q * 8;
 
   // ---- parameter cache (PLDS): this wave's rows' scales/biases, chunk sums
   const size_t row_bytes = static_cast<size_t>(G) * PB;
   const size_t wave_bytes = 32 * row_bytes * (QMODE == ZMOE_Q_AFFINE ? 2 : 1);
-  unsigned char* pw = pcache + wave * wave_bytes * (SWIGLU ? 2 : 1);  // [matrix][s, b][32 rows][G]
+  unsigned char* pw = pcache + wave * wave_bytes * (SWIGLU ? 2 : 1);  // [matrix][s, b][G][32 rows]
   float* pxs = reinterpret_cast<float*>(
       pcache + ((static_cast<size_t>(kGWaves) * wave_bytes * (SWIGLU ? 2 : 1) + 15) & ~static_cast<size_t>(15)));
   if (PLDS) {
@@ -236,28 +242,43 @@ __global__ __launch_bounds__(kGThreads) void k_grouped_qmm(GroupedArgs g) {
       if (!use) continue;
       const int slot = (QMODE == ZMOE_Q_AFFINE) ? m : (m >> 1);
       const uint4* src = reinterpret_cast<const uint4*>(static_cast<const unsigned char*>(srcs[m]) + base_el * PB);
-      uint4* dst = reinterpret_cast<uint4*>(pw + slot * 32 * row_bytes);
-      for (int i = lane; i < nvec; i += kWave) dst[i] = gload(src + i);
+      // stored group-major ([group][row]) so a wave's 32 lanes read 32
+      // consecutive entries of one group
+      unsigned char* dst = pw + slot * 32 * row_bytes;
+      constexpr int per = 16 / PB;  // parameters per 16-byte piece
+      for (int i = lane; i < nvec; i += kWave) {
+        const uint4 v = gload(src + i);
+        const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int t = 0; t < per; ++t) {
+          const int el = i * per + t, row = el / G, gi = el - row * G;
+          const uint32_t word = wv[(t * PB) >> 2];
+          if (PB == 2)
+            reinterpret_cast<uint16_t*>(dst)[gi * 32 + row] = static_cast<uint16_t>(word >> ((t & 1) * 16));
+          else
+            dst[gi * 32 + row] = static_cast<uint8_t>(word >> ((t & 3) * 8));
+        }
+      }
     }
     if (QMODE == ZMOE_Q_AFFINE) {
       // chunk rows' group sums (G floats per row)
       for (int i = threadIdx.x; i < kGChunk * G; i += kGThreads) {
         const int r = i / G, q = i - r * G;
-        pxs[i] = gload(g.asum + act_row(r_begin + r) * G + q);
+        pxs[q * kGChunk + r] = gload(g.asum + act_row(r_begin + r) * G + q);
       }
     }
   }
   auto pscale = [&](int m, int gi) -> float {  // scale of this lane's row, matrix m, group gi
     if (QMODE == ZMOE_Q_AFFINE) {
       const uint16_t* a = reinterpret_cast<const uint16_t*>(pw + (m * 2) * 32 * row_bytes);
-      return bf16_bits_to_f32(a[col * G + gi]);
+      return bf16_bits_to_f32(a[gi * 32 + col]);
     }
-    return e8m0_to_f32(pw[m * 32 * row_bytes + col * G + gi]);
+    return e8m0_to_f32(pw[m * 32 * row_bytes + gi * 32 + col]);
   };
   auto poffset = [&](int m, int gi) -> float {  // affine: b - 128 s
     const uint16_t* sa = reinterpret_cast<const uint16_t*>(pw + (m * 2) * 32 * row_bytes);
     const uint16_t* ba = reinterpret_cast<const uint16_t*>(pw + (m * 2 + 1) * 32 * row_bytes);
-    return bf16_bits_to_f32(ba[col * G + gi]) - 128.0f * bf16_bits_to_f32(sa[col * G + gi]);
+    return bf16_bits_to_f32(ba[gi * 32 + col]) - 128.0f * bf16_bits_to_f32(sa[gi * 32 + col]);
   };
   // this lane's rows in the two MFMA blocks (affine offset operand, no cache)
   const float* as_row[kGBlocksM];
@@ -278,14 +299,15 @@ __global__ __launch_bounds__(kGThreads) void k_grouped_qmm(GroupedArgs g) {
     uint32_t s0[2], s1[2];
     float xs[kGBlocksM];
     uint32_t os0, ob0, os1, ob1;
-    uint4 st;
+    uint4 st[kGStage];
   };
   auto raw_scale = [&](const void* sp, int64_t i) -> uint32_t {
     if (QMODE == ZMOE_Q_AFFINE) return gload(static_cast<const uint16_t*>(sp) + i);
     return gload(static_cast<const uint8_t*>(sp) + i);
   };
   auto load_blk = [&](int blk, KBuf& kb) {
-    kb.st = gload(reinterpret_cast<const uint4*>(st_src + blk * 64));
+#pragma unroll
+    for (int i = 0; i < kGStage; ++i) kb.st[i] = gload(reinterpret_cast<const uint4*>(st_src[i] + blk * 64));
     if (!G32) {
       const uint4 q0 = gload(reinterpret_cast<const uint4*>(W0 + blk * 8 + h * 4));
       kb.w0[0] = q0.x, kb.w0[1] = q0.y, kb.w0[2] = q0.z, kb.w0[3] = q0.w;
@@ -328,15 +350,21 @@ __global__ __launch_bounds__(kGThreads) void k_grouped_qmm(GroupedArgs g) {
   // staged activations are stored already in the operand order: affine pairs
   // (x0,x4) (x1,x5) (x2,x6) (x3,x7)
   auto stage = [&](const KBuf& kb, int buf) {
-    uint4 v = kb.st;
-    if (QMODE == ZMOE_Q_AFFINE) v = __builtin_bit_cast(uint4, act_affine(v));
-    *reinterpret_cast<uint4*>(&alds[buf][st_row * kGLdsRow + st_q * 8]) = v;
+#pragma unroll
+    for (int i = 0; i < kGStage; ++i) {
+      uint4 v = kb.st[i];
+      if (QMODE == ZMOE_Q_AFFINE) v = __builtin_bit_cast(uint4, act_affine(v));
+      *reinterpret_cast<uint4*>(&alds[buf][(st_row + i * (kGThreads / 8)) * kGLdsRow + st_q * 8]) = v;
+    }
   };
   auto decode_scale = [&](uint32_t r) -> float {
     if (QMODE == ZMOE_Q_AFFINE) return bf16_bits_to_f32(r);
     return e8m0_to_f32(r);
   };
-  auto compute_blk = [&](int blk, const KBuf& kb, int buf) {
+  // NMB: the chunk's 32-row MFMA blocks that hold rows (a chunk of <= 32
+  // rows skips the second block's MFMAs and scaling)
+  auto compute_blk = [&](auto nmbc, int blk, const KBuf& kb, int buf) {
+    constexpr int NMB = decltype(nmbc)::value;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const bf16x8_t b0 = wt_operand<QMODE>(kb.w0[j], ak);
@@ -345,7 +373,7 @@ __global__ __launch_bounds__(kGThreads) void k_grouped_qmm(GroupedArgs g) {
       // first k-step of a group starts from a zero accumulator
       const bool fresh = ((blk * 4 + j) % KPG) == 0;
 #pragma unroll
-      for (int mb = 0; mb < kGBlocksM; ++mb) {
+      for (int mb = 0; mb < NMB; ++mb) {
         const uint4 av = *reinterpret_cast<const uint4*>(&alds[buf][(mb * kGTileM + col) * kGLdsRow + koff]);
         const bf16x8_t xa = act_natural(av);
         acc0[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xa, b0, fresh ? f32x16_t{} : acc0[mb], 0, 0, 0);
@@ -364,7 +392,7 @@ __global__ __launch_bounds__(kGThreads) void k_grouped_qmm(GroupedArgs g) {
           if (SWIGLU) s1 = decode_scale(done == 0 ? kb.s1[0] : kb.s1[1]);
         }
 #pragma unroll
-        for (int mb = 0; mb < kGBlocksM; ++mb) {
+        for (int mb = 0; mb < NMB; ++mb) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             tot0[mb][i] = fmaf(s0, acc0[mb][i], tot0[mb][i]);
@@ -382,41 +410,61 @@ __global__ __launch_bounds__(kGThreads) void k_grouped_qmm(GroupedArgs g) {
         c0 = ok ? poffset(0, gi) : 0.0f;
         if (SWIGLU) c1 = ok ? poffset(1, gi) : 0.0f;
 #pragma unroll
-        for (int mb = 0; mb < kGBlocksM; ++mb) xs[mb] = ok ? pxs[(mb * kGTileM + col) * G + gi] : 0.0f;
+        for (int mb = 0; mb < NMB; ++mb) xs[mb] = ok ? pxs[gi * kGChunk + mb * kGTileM + col] : 0.0f;
       } else {
         c0 = bf16_bits_to_f32(kb.ob0) - 128.0f * bf16_bits_to_f32(kb.os0);
         if (SWIGLU) c1 = bf16_bits_to_f32(kb.ob1) - 128.0f * bf16_bits_to_f32(kb.os1);
 #pragma unroll
-        for (int mb = 0; mb < kGBlocksM; ++mb) xs[mb] = kb.xs[mb];
+        for (int mb = 0; mb < NMB; ++mb) xs[mb] = kb.xs[mb];
       }
 #pragma unroll
-      for (int mb = 0; mb < kGBlocksM; ++mb) {
+      for (int mb = 0; mb < NMB; ++mb) {
         tot0[mb] = __builtin_amdgcn_mfma_f32_32x32x2f32(xs[mb], c0, tot0[mb], 0, 0, 0);
         if (SWIGLU) tot1[mb] = __builtin_amdgcn_mfma_f32_32x32x2f32(xs[mb], c1, tot1[mb], 0, 0, 0);
       }
     }
   };
 
-  // three blocks of loads in flight: block s computes from LDS buffer s % 2
-  // while block s + 1 is staged into the other and block s + 2 loads
-  KBuf kb[3];
-  load_blk(0, kb[0]);
-  if (nblk > 1) load_blk(1, kb[1]);
-  stage(kb[0], 0);
-  __syncthreads();
-  auto step = [&](int s, KBuf& cur, KBuf& nxt, KBuf& nxt2) {
-    if (s + 2 < nblk) load_blk(s + 2, nxt2);
-    if (active) compute_blk(s, cur, s & 1);
-    if (s + 1 < nblk) {
-      stage(nxt, (s + 1) & 1);
-      __syncthreads();
+  // NB blocks of loads in flight: block s computes from LDS buffer s % 2
+  // while block s + 1 is staged into the other and blocks up to s + NB - 1
+  // load into registers.  The main loop issues its loads unconditionally
+  // (the block index clamped at the end) so the compiler's wait counts stay
+  // exact across iterations: a load behind a branch makes it fall back to
+  // waiting for every load in flight, which serialises the ring.
+  auto kloop = [&](auto nmbc) {
+    KBuf kb[NB];
+  #pragma unroll
+    for (int i = 0; i < NB - 1; ++i) load_blk(min(i, nblk - 1), kb[i]);
+    stage(kb[0], 0);
+    __syncthreads();
+    int blk = 0;
+    for (; blk + NB < nblk; blk += NB) {
+  #pragma unroll
+      for (int q = 0; q < NB; ++q) {
+        const int s = blk + q;
+        load_blk(min(s + NB - 1, nblk - 1), kb[(q + NB - 1) % NB]);
+        if (active) compute_blk(nmbc, s, kb[q], s & 1);
+        stage(kb[(q + 1) % NB], (s + 1) & 1);
+        __syncthreads();
+      }
+    }
+  #pragma unroll
+    for (int q = 0; q < NB; ++q) {  // the last 1..NB blocks
+      const int s = blk + q;
+      if (s < nblk) {
+        if (s + NB - 1 < nblk) load_blk(s + NB - 1, kb[(q + NB - 1) % NB]);
+        if (active) compute_blk(nmbc, s, kb[q], s & 1);
+        if (s + 1 < nblk) {
+          stage(kb[(q + 1) % NB], (s + 1) & 1);
+          __syncthreads();
+        }
+      }
     }
   };
-  for (int blk = 0; blk < nblk; blk += 3) {
-    step(blk, kb[0], kb[1], kb[2]);
-    if (blk + 1 < nblk) step(blk + 1, kb[1], kb[2], kb[0]);
-    if (blk + 2 < nblk) step(blk + 2, kb[2], kb[0], kb[1]);
-  }
+  if (r_end - r_begin > kGTileM)
+    kloop(std::integral_constant<int, 2>{});
+  else
+    kloop(std::integral_constant<int, 1>{});
   if (!active) return;
   // epilogue: element i of block mb is row mb*32 + (i/4)*8 + h*4 + i%4 of
   // the chunk, column n
@@ -438,21 +486,39 @@ __global__ __launch_bounds__(kGThreads) void k_grouped_qmm(GroupedArgs g) {
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
-template <int QMODE, int GS, bool SWIGLU>
-static void launch_grouped_t(hipStream_t st, const GroupedArgs& g, int n_experts) {
-  const int ntiles = (g.N + kGTileN - 1) / kGTileN;
-  const int units = grouped_max_blocks(g.M, n_experts);
-  const size_t pc = grouped_pcache_bytes(QMODE, SWIGLU, g.K / GS);
-  if (pc <= kGPcacheMax) {
+template <int QMODE, int GS, bool SWIGLU, bool PLDS, int NB>
+static void launch_grouped_nb(hipStream_t st, const GroupedArgs& g, unsigned blocks, size_t lds) {
+  if (PLDS) {
     static bool prepared = false;
     if (!prepared) {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_grouped_qmm<QMODE, GS, SWIGLU, true>),
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_grouped_qmm<QMODE, GS, SWIGLU, PLDS, NB>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kGPcacheMax));
       prepared = true;
     }
-    hipLaunchKernelGGL((k_grouped_qmm<QMODE, GS, SWIGLU, true>), dim3(units * ntiles), dim3(kGThreads), pc, st, g);
+  }
+  hipLaunchKernelGGL((k_grouped_qmm<QMODE, GS, SWIGLU, PLDS, NB>), dim3(blocks), dim3(kGThreads), lds, st, g);
+}
+
+template <int QMODE, int GS, bool SWIGLU>
+static void launch_grouped_t(hipStream_t st, const GroupedArgs& g, int n_experts) {
+  const int ntiles = (g.N + kGTileN - 1) / kGTileN;
+  const unsigned blocks = static_cast<unsigned>(grouped_max_blocks(g.M, n_experts) * ntiles);
+  const size_t pc = grouped_pcache_bytes(QMODE, SWIGLU, g.K / GS);
+  if (pc <= kGPcacheMax) {
+    // with the parameter cache the workgroup holds a CU's LDS alone; its
+    // register budget then allows a deeper load ring for gate/up
+    static int nb = -1;
+    if (nb < 0) {
+      const char* e = getenv("ZMOE_GNB");
+      nb = e ? atoi(e) : 5;
+    }
+    if constexpr (QMODE == ZMOE_Q_AFFINE && SWIGLU) {  // (mxfp4 would spill)
+      if (nb == 4) return launch_grouped_nb<QMODE, GS, SWIGLU, true, 4>(st, g, blocks, pc);
+      if (nb == 5) return launch_grouped_nb<QMODE, GS, SWIGLU, true, 5>(st, g, blocks, pc);
+    }
+    launch_grouped_nb<QMODE, GS, SWIGLU, true, 3>(st, g, blocks, pc);
   } else {
-    hipLaunchKernelGGL((k_grouped_qmm<QMODE, GS, SWIGLU, false>), dim3(units * ntiles), dim3(kGThreads), 0, st, g);
+    launch_grouped_nb<QMODE, GS, SWIGLU, false, 3>(st, g, blocks, 0);
   }
 }
 

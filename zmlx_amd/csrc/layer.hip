@@ -172,7 +172,10 @@ extern "C" int zmoe_moe_layer(void* stream, const zmoe_layer_desc* d, const void
   ZMOE_REQUIRE(d->bits == 4, ZMOE_EUNSUPPORTED, "[moe_layer] only 4-bit weights.");
 
   // 1. router projection (bf16 logits, as the gate nn.Linear returns them)
-  rc = zmoe_dense_logits(stream, x, d->router_w, B, E, H, ZMOE_DT_BF16, ws.logits);
+  // (prefill batches on MFMA; decode batches keep the chunk order that the
+  // single-launch kernels reproduce)
+  rc = use_grouped(d, B) && H % 2048 == 0 ? launch_logits_mfma(st, x, d->router_w, B, E, H, ZMOE_DT_BF16, ws.logits)
+                         : zmoe_dense_logits(stream, x, d->router_w, B, E, H, ZMOE_DT_BF16, ws.logits);
   if (rc) return rc;
   // 2. gating
   int w_dtype = ZMOE_DT_BF16;

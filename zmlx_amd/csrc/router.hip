@@ -181,6 +181,89 @@ extern "C" int zmoe_dense_logits(void* stream, const void* x, const void* w, int
   return check_launch("dense_logits");
 }
 
+// ---------------------------------------------------------------------------
+// Router projection for prefill batches on MFMA: a workgroup of 8 waves owns
+// a 16-token x 16-expert tile (256 workgroups at 512 tokens x 128 experts, so
+// every CU streams its share); wave w of 8 takes the k range
+// [w*H/8, (w+1)*H/8) with v_mfma_f32_16x16x32_bf16 (bf16 products exact, fp32
+// accumulation) and the 8 partial tiles are added in wave order through LDS.
+// Used by the layer for batches on the grouped path, where no single-launch
+// kernel has to reproduce its logits bit for bit.
+// ---------------------------------------------------------------------------
+typedef __bf16 lg_bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float lg_f32x4_t __attribute__((ext_vector_type(4)));
+constexpr int kLgSteps = 4;  // k-steps of 32 per load batch
+constexpr int kLgWaves = 8;  // waves per tile, each a k range
+
+__global__ __launch_bounds__(512) void k_logits_mfma(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                     int B, int E, int H, int out_f32, void* __restrict__ out) {
+  __shared__ float red[kLgWaves - 1][kWave][5];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int q = lane >> 4, col = lane & 15;  // k quarter (8 of every 32 k), row in the tile
+  const int b0 = blockIdx.x * 16, e0 = blockIdx.y * 16;
+  const int64_t xr = min(b0 + col, B - 1), wr = min(e0 + col, E - 1);
+  const int kq = H / kLgWaves;  // k per wave
+  const uint16_t* xp = x + xr * H + wave * kq + q * 8;
+  const uint16_t* wp = w + wr * H + wave * kq + q * 8;
+  const int nch = kq / (32 * kLgSteps);  // load batches per wave (even)
+  lg_f32x4_t acc = {};
+  // two register buffers in ping-pong, loads issued unconditionally (the
+  // batch index clamped) so the compiler's wait counts stay exact
+  uint4 xa[kLgSteps], wa[kLgSteps], xb[kLgSteps], wb[kLgSteps];
+  auto load = [&](uint4* xv, uint4* wv, int c) {
+#pragma unroll
+    for (int i = 0; i < kLgSteps; ++i) {
+      xv[i] = gload(reinterpret_cast<const uint4*>(xp + (c * kLgSteps + i) * 32));
+      wv[i] = gload(reinterpret_cast<const uint4*>(wp + (c * kLgSteps + i) * 32));
+    }
+  };
+  auto mfma = [&](const uint4* xv, const uint4* wv) {
+#pragma unroll
+    for (int i = 0; i < kLgSteps; ++i)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(lg_bf16x8_t, xv[i]),
+                                                    __builtin_bit_cast(lg_bf16x8_t, wv[i]), acc, 0, 0, 0);
+  };
+  load(xa, wa, 0);
+  for (int c = 0; c < nch; c += 2) {
+    load(xb, wb, c + 1);
+    mfma(xa, wa);
+    load(xa, wa, min(c + 2, nch - 1));
+    mfma(xb, wb);
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave - 1][lane][i] = acc[i];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  // element i of the 16x16 tile: token row 4*q + i, expert column col
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float v = acc[i];
+#pragma unroll
+    for (int r = 0; r < kLgWaves - 1; ++r) v += red[r][lane][i];
+    const int b = b0 + q * 4 + i, e = e0 + col;
+    if (b < B && e < E) {
+      const int64_t o = static_cast<int64_t>(b) * E + e;
+      if (out_f32)
+        static_cast<float*>(out)[o] = v;
+      else
+        static_cast<uint16_t*>(out)[o] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+    }
+  }
+}
+
+int zmoe::launch_logits_mfma(hipStream_t st, const void* x, const void* w, int B, int E, int H, int out_dtype,
+                             void* out) {
+  ZMOE_REQUIRE(H % (2 * kLgWaves * kLgSteps * 32) == 0, ZMOE_EINVAL_SHAPE,
+               "[dense_logits] hidden must be a multiple of 2048.");
+  if (B == 0) return ZMOE_OK;
+  hipLaunchKernelGGL(k_logits_mfma, dim3((B + 15) / 16, (E + 15) / 16), dim3(kLgWaves * kWave), 0, st,
+                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), B, E, H,
+                     out_dtype == ZMOE_DT_F32 ? 1 : 0, out);
+  return check_launch("dense_logits (mfma)");
+}
+
 extern "C" int zmoe_router_softmax_topk(void* stream, const void* logits, int B, int E, int k, int norm_topk_prob,
                                         void* out_w, uint32_t* out_idx) {
   int rc = check_router("router_softmax_topk", B, E, k);
