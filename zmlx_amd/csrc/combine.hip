@@ -34,10 +34,101 @@ __global__ __launch_bounds__(256) void k_moe_combine(const uint16_t* __restrict_
   }
 }
 
+// One k-step and the final rounding of combine_one's modes, for a thread that
+// owns 8 consecutive outputs: the same operations in the same k order, so the
+// results are bit-identical to combine_one.
+__device__ __forceinline__ float combine_step(int mode, float acc, float w, float y) {
+  switch (mode) {
+    case ZMOE_COMBINE_NATIVE:
+      return add_nofma(acc, round_bf16(mul_nofma(w, y)));
+    case ZMOE_COMBINE_FP32:
+    case ZMOE_COMBINE_FLOAT:
+      return fmaf(w, y, acc);
+    case ZMOE_COMBINE_FP32_NO_FMA:
+    case ZMOE_COMBINE_NO_FMA:
+      return add_nofma(acc, mul_nofma(w, y));
+    default:  // ZMOE_COMBINE_EXACT
+      return round_bf16(add_nofma(acc, round_bf16(mul_nofma(round_bf16(w), y))));
+  }
+}
+__device__ __forceinline__ float combine_finish(int mode, float acc) {
+  return (mode == ZMOE_COMBINE_NATIVE || mode == ZMOE_COMBINE_FLOAT || mode == ZMOE_COMBINE_NO_FMA) ? round_bf16(acc)
+                                                                                                   : acc;
+}
+
+// D % 8 == 0 and K <= kCombVecMaxK: thread owns outputs d0 .. d0 + 7 and
+// reads 16 bytes per expert.  KT > 0 is the expert count at compile time;
+// KT = 0 takes K at run time (loads clamped to K - 1).
+constexpr int kCombVecMaxK = 16;
+template <int KT>
+__global__ __launch_bounds__(256) void k_moe_combine8(const uint16_t* __restrict__ y, const void* __restrict__ w,
+                                                      int w_dtype, int K, int D, int mode, int force_bf16,
+                                                      const uint16_t* __restrict__ shared, void* __restrict__ out) {
+  const int d0 = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  const int64_t b = blockIdx.y;
+  if (d0 >= D) return;
+  float acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+  // every expert's 16 bytes are loaded at once (indices clamped, loads
+  // unconditional) so the kernel is one memory round trip deep
+  constexpr int NK = KT > 0 ? KT : kCombVecMaxK;
+  if (KT > 0) K = KT;
+  uint4 v[NK];
+  float wk[NK];
+#pragma unroll
+  for (int k = 0; k < NK; ++k) {
+    const int kc = KT > 0 ? k : min(k, K - 1);
+    v[k] = gload(reinterpret_cast<const uint4*>(y + (b * K + kc) * D + d0));
+    wk[k] = load_w(w, w_dtype, b * K + kc);
+  }
+#pragma unroll
+  for (int k = 0; k < NK; ++k) {
+    if (KT > 0 || k < K) {
+      const uint32_t wv[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        acc[j] = combine_step(mode, acc[j], wk[k], bf16_bits_to_f32((wv[j >> 1] >> ((j & 1) * 16)) & 0xFFFFu));
+    }
+  }
+  if (combine_f32_out(mode) && !force_bf16) {
+    float* o = static_cast<float*>(out) + b * D + d0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = combine_finish(mode, acc[j]);
+  } else {
+    uint4 sh = make_uint4(0, 0, 0, 0);
+    if (shared) sh = gload(reinterpret_cast<const uint4*>(shared + b * D + d0));
+    const uint32_t sv[4] = {sh.x, sh.y, sh.z, sh.w};
+    uint32_t ov[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t pair = 0;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int j = q * 2 + hh;
+        float r = round_bf16(combine_finish(mode, acc[j]));
+        if (shared) r = add_nofma(r, bf16_bits_to_f32((sv[q] >> (hh * 16)) & 0xFFFFu));
+        pair |= f32_to_bf16_bits(r) << (hh * 16);
+      }
+      ov[q] = pair;
+    }
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + b * D + d0) = make_uint4(ov[0], ov[1], ov[2], ov[3]);
+  }
+}
+
 int launch_combine(hipStream_t st, const void* y, const void* w, int w_dtype, int B, int K, int D, int mode,
                    int force_bf16, const void* shared, void* out) {
-  hipLaunchKernelGGL(k_moe_combine, dim3((D + 255) / 256, B), dim3(256), 0, st, static_cast<const uint16_t*>(y), w,
-                     w_dtype, K, D, mode, force_bf16, static_cast<const uint16_t*>(shared), out);
+  const bool vec = D % 8 == 0 && K <= kCombVecMaxK && (reinterpret_cast<uintptr_t>(y) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(out) & 15) == 0 && (reinterpret_cast<uintptr_t>(shared) & 15) == 0;
+  if (vec) {
+    auto fn = K == 8 ? k_moe_combine8<8> : K == 4 ? k_moe_combine8<4> : K == 2 ? k_moe_combine8<2>
+            : K == 1 ? k_moe_combine8<1> : k_moe_combine8<0>;
+    hipLaunchKernelGGL(fn, dim3((D / 8 + 255) / 256, B), dim3(256), 0, st, static_cast<const uint16_t*>(y), w, w_dtype,
+                       K, D, mode, force_bf16, static_cast<const uint16_t*>(shared), out);
+  } else {
+    hipLaunchKernelGGL(k_moe_combine, dim3((D + 255) / 256, B), dim3(256), 0, st, static_cast<const uint16_t*>(y), w,
+                       w_dtype, K, D, mode, force_bf16, static_cast<const uint16_t*>(shared), out);
+  }
   return check_launch("moe_combine");
 }
 

@@ -61,37 +61,45 @@ __global__ __launch_bounds__(1024) void k_sort_pairs(const uint32_t* __restrict_
                                                      int* __restrict__ blocks) {
   __shared__ int cnt[1024];
   __shared__ int off[1025];
+  __shared__ int cst[1024];  // first chunk of each expert
+  __shared__ int wtot[2][16];
   for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
   __syncthreads();
   for (int q = threadIdx.x; q < npairs; q += blockDim.x) atomicAdd(&cnt[min(static_cast<int>(idx[q]), E - 1)], 1);
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int run = 0;
-    for (int e = 0; e < E; ++e) {
-      off[e] = run;
-      run += cnt[e];
+  // exclusive scans of the pair counts and the chunk counts, thread e owns
+  // expert e (E <= 1024): per-wave shuffle scans, then the wave totals
+  {
+    const int e = threadIdx.x, lane = e & (kWave - 1), wv = e / kWave;
+    const int c = e < E ? cnt[e] : 0;
+    const int nc = (c + kGChunk - 1) / kGChunk;
+    int ic = c, inc = nc;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int t0 = __shfl_up(ic, o), t1 = __shfl_up(inc, o);
+      if (lane >= o) ic += t0, inc += t1;
     }
-    off[E] = run;
+    if (lane == kWave - 1) wtot[0][wv] = ic, wtot[1][wv] = inc;
+    __syncthreads();
+    int bc = 0, bnc = 0;
+    for (int w = 0; w < wv; ++w) bc += wtot[0][w], bnc += wtot[1][w];
+    if (e < E) {
+      off[e] = bc + ic - c;
+      cst[e] = bnc + inc - nc;
+    }
+    if (e == E - 1) {
+      off[E] = bc + ic;
+      if (blocks) offsets[E + 1] = bnc + inc;
+    }
   }
   __syncthreads();
   for (int e = threadIdx.x; e <= E; e += blockDim.x) offsets[e] = off[e];
   if (blocks) {
-    // chunks of kGChunk rows of every expert, in expert order (their starts
-    // reuse cnt)
-    if (threadIdx.x == 0) {
-      int nb = 0;
-      for (int e = 0; e < E; ++e) {
-        cnt[e] = nb;
-        nb += (off[e + 1] - off[e] + kGChunk - 1) / kGChunk;
-      }
-      offsets[E + 1] = nb;
-    }
-    __syncthreads();
+    // chunks of kGChunk rows of every expert, in expert order
     for (int e = threadIdx.x; e < E; e += blockDim.x) {
       const int nbe = (off[e + 1] - off[e] + kGChunk - 1) / kGChunk;
-      for (int j = 0; j < nbe; ++j) blocks[cnt[e] + j] = e | (j << 11);
+      for (int j = 0; j < nbe; ++j) blocks[cst[e] + j] = e | (j << 11);
     }
-    __syncthreads();
   }
   for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
   __syncthreads();
