@@ -16,15 +16,48 @@ __device__ __forceinline__ float load_w(const void* w, int dtype, int64_t i) {
 // force_bf16: write bf16 even for the fp32 modes (the caller's .astype(bf16));
 // shared (nullable): bf16 [B, D] addend applied to the bf16 result
 // (``y + shared_experts(x)``, moe_mlp.py:1059-1061).
-__global__ __launch_bounds__(256) void k_moe_combine(const uint16_t* __restrict__ y, const void* __restrict__ w,
-                                                     int w_dtype, int K, int D, int mode, int force_bf16,
-                                                     const uint16_t* __restrict__ shared, void* __restrict__ out) {
+constexpr int kCombMaxK = 16;  // experts per token of the unrolled kernels
+
+// any K (no unrolling): one expert at a time
+__global__ __launch_bounds__(256) void k_moe_combine_any(const uint16_t* __restrict__ y, const void* __restrict__ w,
+                                                         int w_dtype, int K, int D, int mode, int force_bf16,
+                                                         const uint16_t* __restrict__ shared, void* __restrict__ out) {
   const int d = blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t b = blockIdx.y;
   if (d >= D) return;
   const float v = combine_one(
       mode, K, [&](int k) { return bf16_bits_to_f32(y[(b * K + k) * D + d]); },
       [&](int k) { return load_w(w, w_dtype, b * K + k); });
+  if (combine_f32_out(mode) && !force_bf16) {
+    static_cast<float*>(out)[b * D + d] = v;
+  } else {
+    float r = round_bf16(v);
+    if (shared) r = add_nofma(r, bf16_bits_to_f32(shared[b * D + d]));
+    static_cast<uint16_t*>(out)[b * D + d] = static_cast<uint16_t>(f32_to_bf16_bits(r));
+  }
+}
+
+template <int KT, bool WF32>
+__global__ __launch_bounds__(256) void k_moe_combine(const uint16_t* __restrict__ y, const void* __restrict__ w,
+                                                     int w_dtype, int K, int D, int mode, int force_bf16,
+                                                     const uint16_t* __restrict__ shared, void* __restrict__ out) {
+  const int d = blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t b = blockIdx.y;
+  if (d >= D) return;
+  // every expert's value and weight loaded at once (KT = 0: K at run time,
+  // indices clamped; the weight dtype is fixed at compile time because a load
+  // behind a dtype branch makes the compiler wait for it)
+  constexpr int NK = KT > 0 ? KT : kCombMaxK;
+  if (KT > 0) K = KT;
+  float yv[NK], wv[NK];
+#pragma unroll
+  for (int k = 0; k < NK; ++k) {
+    const int kc = KT > 0 ? k : min(k, K - 1);
+    yv[k] = bf16_bits_to_f32(y[(b * K + kc) * D + d]);
+    wv[k] = WF32 ? static_cast<const float*>(w)[b * K + kc]
+                 : bf16_bits_to_f32(static_cast<const uint16_t*>(w)[b * K + kc]);
+  }
+  const float v = combine_one(mode, K, [&](int k) { return yv[k]; }, [&](int k) { return wv[k]; });
   if (combine_f32_out(mode) && !force_bf16) {
     static_cast<float*>(out)[b * D + d] = v;
   } else {
@@ -58,10 +91,11 @@ __device__ __forceinline__ float combine_finish(int mode, float acc) {
 
 // D % 8 == 0 and K <= kCombVecMaxK: thread owns outputs d0 .. d0 + 7 and
 // reads 16 bytes per expert.  KT > 0 is the expert count at compile time;
-// KT = 0 takes K at run time (loads clamped to K - 1).
-constexpr int kCombVecMaxK = 16;
-template <int KT>
-__global__ __launch_bounds__(256) void k_moe_combine8(const uint16_t* __restrict__ y, const void* __restrict__ w,
+// KT = 0 takes K at run time (loads clamped to K - 1); WF32: f32 weights
+// (else bf16).
+constexpr int kCombVecMaxK = kCombMaxK;
+template <int KT, bool WF32>
+__global__ __launch_bounds__(64) void k_moe_combine8(const uint16_t* __restrict__ y, const void* __restrict__ w,
                                                       int w_dtype, int K, int D, int mode, int force_bf16,
                                                       const uint16_t* __restrict__ shared, void* __restrict__ out) {
   const int d0 = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
@@ -80,7 +114,10 @@ __global__ __launch_bounds__(256) void k_moe_combine8(const uint16_t* __restrict
   for (int k = 0; k < NK; ++k) {
     const int kc = KT > 0 ? k : min(k, K - 1);
     v[k] = gload(reinterpret_cast<const uint4*>(y + (b * K + kc) * D + d0));
-    wk[k] = load_w(w, w_dtype, b * K + kc);
+    // dtype fixed at compile time: a load behind a dtype branch would make
+    // the compiler wait for it before issuing the next
+    wk[k] = WF32 ? static_cast<const float*>(w)[b * K + kc]
+                 : bf16_bits_to_f32(static_cast<const uint16_t*>(w)[b * K + kc]);
   }
 #pragma unroll
   for (int k = 0; k < NK; ++k) {
@@ -118,16 +155,32 @@ __global__ __launch_bounds__(256) void k_moe_combine8(const uint16_t* __restrict
 
 int launch_combine(hipStream_t st, const void* y, const void* w, int w_dtype, int B, int K, int D, int mode,
                    int force_bf16, const void* shared, void* out) {
-  const bool vec = D % 8 == 0 && K <= kCombVecMaxK && (reinterpret_cast<uintptr_t>(y) & 15) == 0 &&
+  // the 8-wide kernel pays off for prefill-sized batches; small batches
+  // keep one output per thread (more waves in flight)
+  const bool vec = B >= 64 && D % 8 == 0 && K <= kCombVecMaxK && (reinterpret_cast<uintptr_t>(y) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(out) & 15) == 0 && (reinterpret_cast<uintptr_t>(shared) & 15) == 0;
   if (vec) {
-    auto fn = K == 8 ? k_moe_combine8<8> : K == 4 ? k_moe_combine8<4> : K == 2 ? k_moe_combine8<2>
-            : K == 1 ? k_moe_combine8<1> : k_moe_combine8<0>;
-    hipLaunchKernelGGL(fn, dim3((D / 8 + 255) / 256, B), dim3(256), 0, st, static_cast<const uint16_t*>(y), w, w_dtype,
+    const bool f = w_dtype == ZMOE_DT_F32;
+    auto fn = K == 8   ? (f ? k_moe_combine8<8, true> : k_moe_combine8<8, false>)
+              : K == 4 ? (f ? k_moe_combine8<4, true> : k_moe_combine8<4, false>)
+              : K == 2 ? (f ? k_moe_combine8<2, true> : k_moe_combine8<2, false>)
+              : K == 1 ? (f ? k_moe_combine8<1, true> : k_moe_combine8<1, false>)
+                       : (f ? k_moe_combine8<0, true> : k_moe_combine8<0, false>);
+    // one wave per 512 outputs, so small batches still spread over the CUs
+    hipLaunchKernelGGL(fn, dim3((D / 8 + 63) / 64, B), dim3(64), 0, st, static_cast<const uint16_t*>(y), w, w_dtype,
                        K, D, mode, force_bf16, static_cast<const uint16_t*>(shared), out);
+  } else if (K <= kCombMaxK) {
+    const bool f = w_dtype == ZMOE_DT_F32;
+    auto fn = K == 8   ? (f ? k_moe_combine<8, true> : k_moe_combine<8, false>)
+              : K == 4 ? (f ? k_moe_combine<4, true> : k_moe_combine<4, false>)
+              : K == 2 ? (f ? k_moe_combine<2, true> : k_moe_combine<2, false>)
+              : K == 1 ? (f ? k_moe_combine<1, true> : k_moe_combine<1, false>)
+                       : (f ? k_moe_combine<0, true> : k_moe_combine<0, false>);
+    hipLaunchKernelGGL(fn, dim3((D + 255) / 256, B), dim3(256), 0, st, static_cast<const uint16_t*>(y), w, w_dtype, K,
+                       D, mode, force_bf16, static_cast<const uint16_t*>(shared), out);
   } else {
-    hipLaunchKernelGGL(k_moe_combine, dim3((D + 255) / 256, B), dim3(256), 0, st, static_cast<const uint16_t*>(y), w,
-                       w_dtype, K, D, mode, force_bf16, static_cast<const uint16_t*>(shared), out);
+    hipLaunchKernelGGL(k_moe_combine_any, dim3((D + 255) / 256, B), dim3(256), 0, st, static_cast<const uint16_t*>(y),
+                       w, w_dtype, K, D, mode, force_bf16, static_cast<const uint16_t*>(shared), out);
   }
   return check_launch("moe_combine");
 }
