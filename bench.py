@@ -13,14 +13,15 @@ A step = one pass of the MoE block over the batch through all 48 layer copies
   value       us per token per layer call at B (lower is better)
   gbps        algorithmic HBM bytes per layer call / layer time
   roofline    of the dominant kernel -- the single-launch layer kernel
-              k_moe_decode, one launch per layer call -- from HIP events on
+              k_moe_decode1, one launch per layer call -- from HIP events on
               the stream it runs on, around the timed region; `traffic` is the
               measured HBM bytes per launch from the committed rocprofv3
-              counter summary (profiles/k_moe_decode_qwen3_b1_traffic.json)
+              counter summary (profiles/k_moe_decode1_qwen3_b1_traffic.json)
   cpu_baseline  this repo's C++/OpenMP restatement of the unpatched MLX path
               (MLX is not installable offline) on the host cores, rank 0.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B]
+       python bench.py --all-configs          # + LFM2, GLM-mxfp4, DeepSeek-V3 lines
        python bench.py --profile-run          # short run for rocprofv3 --pmc
        python bench.py --summarize-pmc DIR     # FETCH_SIZE/WRITE_SIZE -> traffic
 """
@@ -289,6 +290,87 @@ def cpu_baseline(base, layer0, x_host, budget_s: float = 12.0, max_tokens: int =
     }
 
 
+# The other BASELINE configs (measured with --all-configs; not the headline
+# value): name -> (family, H, E, K, I, quant mode, group size, shared I,
+# router kwargs, batches, layer copies).  Copies are clones of one generated
+# bank, so every call reads its own weights from HBM (>= 8 copies, working
+# sets well above the 256 MB Infinity Cache).
+OTHER_CONFIGS = {
+    "lfm2_8b_a1b": ("lfm2", 2048, 32, 4, 1792, "affine", 64, 0, {}, (1,), 8),
+    "glm_4.7_flash_mxfp4": ("glm", 2048, 64, 4, 1536, "mxfp4", 32, 1536, {"routed_scaling_factor": 1.8}, (1, 8), 8),
+    "deepseek_v3": ("deepseek", 7168, 256, 8, 2048, "affine", 64, 2048,
+                    {"n_group": 8, "topk_group": 4, "routed_scaling_factor": 2.5}, (1, 64), 8),
+}
+
+
+def expert_bytes(h, i, mode, gs) -> int:
+    if mode == "affine":
+        return 2 * i * (h // 2 + (h // gs) * 4) + h * (i // 2 + (i // gs) * 4)
+    return 2 * i * (h // 2 + h // 32) + h * (i // 2 + i // 32)
+
+
+def other_config_lines(dev, steps: int, warmup: int) -> dict:
+    """Per-config lines: us per layer call, algorithmic GB/s and the fraction
+    of the 8 TB/s roofline at each of the config's batch sizes."""
+    import torch
+
+    from zmlx_amd.layer import QuantizedMoELayer, QuantProj
+    from zmlx_amd.quant import quantize_affine, quantize_mxfp4
+
+    out = {}
+    g = torch.Generator(device=dev)
+    g.manual_seed(77)
+    for name, (fam, h, e, k, i, mode, gs, shi, kw, batches, copies) in OTHER_CONFIGS.items():
+        log(f"{name}: building {copies} layer copies")
+
+        def bank(n_exp, n_out, n_in):
+            ws, ss, bs = [], [], []
+            for e0 in range(0, n_exp, 16):
+                w = (torch.randn((min(16, n_exp - e0), n_out, n_in), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+                if mode == "affine":
+                    q, sc, bi = quantize_affine(w, gs)
+                else:
+                    (q, sc), bi = quantize_mxfp4(w), None
+                ws.append(q), ss.append(sc), bs.append(bi)
+            return torch.cat(ws), torch.cat(ss), (torch.cat(bs) if bs[0] is not None else None)
+
+        base = {"gate": bank(e, i, h), "up": bank(e, i, h), "down": bank(e, h, i)}
+        sh = {"gate": bank(1, shi, h), "up": bank(1, shi, h), "down": bank(1, h, shi)} if shi else None
+        layers = []
+        for _ in range(copies):
+            cp = {n: tuple(None if t is None else t.clone() for t in v) for n, v in base.items()}
+            shared = None
+            if sh is not None:
+                shared = tuple(QuantProj(v[0][0].clone(), v[1][0].clone(), None if v[2] is None else v[2][0].clone())
+                               for v in (sh["gate"], sh["up"], sh["down"]))
+            wr = (torch.randn((e, h), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+            bias = (torch.randn((e,), generator=g, device=dev) * 0.05) if fam in ("glm", "deepseek") else None
+            layers.append(QuantizedMoELayer.for_family(
+                fam, wr, *(QuantProj(*cp[n]) for n in ("gate", "up", "down")), top_k=k, router_bias=bias,
+                group_size=gs, mode=mode, shared=shared, **kw))
+        torch.cuda.synchronize()
+        for B in batches:
+            x = torch.randn((B, h), generator=g, device=dev).to(torch.bfloat16)
+            uniq = []
+            for layer in layers:
+                _, idx, _ = layer(x, return_routing=True)
+                uniq.append(int(torch.unique(idx).numel()))
+            ms = time_layers(layers, x, steps, warmup)
+            us = ms * 1e3 / len(layers)
+            avg_u = sum(uniq) / len(uniq)
+            alg = avg_u * expert_bytes(h, i, mode, gs) + (expert_bytes(h, shi, mode, gs) if shi else 0) \
+                + e * h * 2 + 4 * B * h
+            gbps = alg / (us * 1e-6) / 1e9
+            out[f"{name}_b{B}"] = {"us_per_layer_call": round(us, 3), "us_per_token": round(us / B, 3),
+                                   "gbps": round(gbps, 1), "roofline_frac": round(gbps / HBM_PEAK_GBPS, 4),
+                                   "unique_experts": round(avg_u, 2), "alg_bytes_per_call": int(alg),
+                                   "layer_copies": copies, "steps": steps}
+            log(f"{name} B={B}: {out[f'{name}_b{B}']}")
+        del layers, base, sh
+        torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -299,6 +381,8 @@ def main() -> int:
     ap.add_argument("--extra-batches", default="4,16")
     ap.add_argument("--prefill", type=int, default=512,
                     help="tokens of the prefill line (config 4; 0 skips it)")
+    ap.add_argument("--all-configs", action="store_true",
+                    help="also measure the other BASELINE configs (LFM2, GLM-mxfp4, DeepSeek-V3)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
@@ -363,6 +447,11 @@ def main() -> int:
     if args.prefill > 0:
         per_b["prefill"] = prefill_line(layers, args.prefill, gen, dev, max(3, args.steps // 10), args.warmup)
         log(f"prefill: {per_b['prefill']}")
+
+    if args.all_configs:
+        layers = layers[:1]  # the CPU baseline reads the first copy
+        torch.cuda.empty_cache()
+        per_b["configs"] = other_config_lines(dev, max(5, args.steps // 5), args.warmup)
 
     cpu = None
     if not args.no_cpu_baseline:

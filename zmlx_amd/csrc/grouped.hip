@@ -56,7 +56,7 @@ constexpr int kGStage = kGChunk * 8 / kGThreads;  // 16-byte staging pieces per 
 // ---------------------------------------------------------------------------
 // sort (token, k) pairs by expert: one workgroup, counts in LDS
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(1024) void k_sort_pairs(const uint32_t* __restrict__ idx, int npairs, int E,
+__global__ __launch_bounds__(1024) void k_sort_pairs(const uint32_t* __restrict__ idx, int npairs, int E, int chunk,
                                                      int* __restrict__ offsets, int* __restrict__ sorted,
                                                      int* __restrict__ blocks) {
   __shared__ int cnt[1024];
@@ -72,7 +72,7 @@ __global__ __launch_bounds__(1024) void k_sort_pairs(const uint32_t* __restrict_
   {
     const int e = threadIdx.x, lane = e & (kWave - 1), wv = e / kWave;
     const int c = e < E ? cnt[e] : 0;
-    const int nc = (c + kGChunk - 1) / kGChunk;
+    const int nc = (c + chunk - 1) / chunk;
     int ic = c, inc = nc;
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) {
@@ -95,9 +95,9 @@ __global__ __launch_bounds__(1024) void k_sort_pairs(const uint32_t* __restrict_
   __syncthreads();
   for (int e = threadIdx.x; e <= E; e += blockDim.x) offsets[e] = off[e];
   if (blocks) {
-    // chunks of kGChunk rows of every expert, in expert order
+    // chunks of `chunk` rows of every expert, in expert order
     for (int e = threadIdx.x; e < E; e += blockDim.x) {
-      const int nbe = (off[e + 1] - off[e] + kGChunk - 1) / kGChunk;
+      const int nbe = (off[e + 1] - off[e] + chunk - 1) / chunk;
       for (int j = 0; j < nbe; ++j) blocks[cst[e] + j] = e | (j << 11);
     }
   }
@@ -530,6 +530,10 @@ static void launch_grouped_t(hipStream_t st, const GroupedArgs& g, int n_experts
   }
 }
 
+bool grouped_params_cached(int quant_mode, bool swiglu, int K, int gs) {
+  return grouped_pcache_bytes(quant_mode, swiglu, K / (quant_mode == ZMOE_Q_AFFINE ? gs : 32)) <= kGPcacheMax;
+}
+
 int launch_grouped(hipStream_t st, const GroupedArgs& g, int n_experts, int quant_mode, bool swiglu) {
   if (quant_mode == ZMOE_Q_AFFINE) {
     switch (g.gs) {
@@ -552,8 +556,9 @@ int launch_grouped(hipStream_t st, const GroupedArgs& g, int n_experts, int quan
   return check_launch("grouped gather_qmm");
 }
 
-int launch_sort_pairs(hipStream_t st, const uint32_t* idx, int npairs, int E, int* offsets, int* sorted, int* blocks) {
-  hipLaunchKernelGGL(k_sort_pairs, dim3(1), dim3(1024), 0, st, idx, npairs, E, offsets, sorted, blocks);
+int launch_sort_pairs(hipStream_t st, const uint32_t* idx, int npairs, int E, int* offsets, int* sorted, int* blocks,
+                      int chunk) {
+  hipLaunchKernelGGL(k_sort_pairs, dim3(1), dim3(1024), 0, st, idx, npairs, E, chunk, offsets, sorted, blocks);
   return check_launch("sort pairs by expert");
 }
 

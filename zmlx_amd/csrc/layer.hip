@@ -13,11 +13,24 @@ namespace zmoe {
 
 static size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
-// Batches of at least this many tokens run the routed experts as grouped
-// GEMMs on MFMA (pairs sorted by expert; the reference's mlx_lm SwitchGLU
-// sorts from 64 indices on, moe_mlp.py:540-543); smaller ones as GEMVs.
-// ZMOE_GROUPED_MIN_B overrides it.
+// How the kernel sequence runs the routed experts (the reference's mlx_lm
+// SwitchGLU sorts the pairs by expert from 64 indices on,
+// moe_mlp.py:540-543):
+//   per-pair GEMV    below kGroupedGemvMinB tokens, or while the experts
+//                    average under kGroupedGemvRowsMin rows: each (token, k)
+//                    pair streams its expert's rows (k_gather_qmv);
+//   expert-major GEMV (pairs sorted by expert): each expert's rows are read
+//                    once per 4 of its rows (k_grouped_qmv);
+//   grouped MFMA GEMM from kGroupedMinB tokens when the experts average at
+//                    least kGroupedMfmaRows rows or its parameters fit the
+//                    LDS cache (k_grouped_qmm).
+// ZMOE_GROUPED_MIN_B overrides kGroupedMinB; ZMOE_GROUPED_GEMV=0 turns the
+// expert-major GEMV off.
 constexpr int kGroupedMinB = 32;
+constexpr int kGroupedGemvMinB = 9;
+constexpr int kGroupedMfmaRows = 16;
+constexpr int kGroupedGemvRowsMin = 2;
+enum SeqMode { kSeqPairs = 0, kSeqGemv = 1, kSeqMfma = 2 };
 
 static int grouped_min_b() {
   static int v = -1;
@@ -29,8 +42,32 @@ static int grouped_min_b() {
   return v;
 }
 
+static bool gemv_enabled() {
+  static int v = -1;
+  if (v < 0) {
+    const char* e = getenv("ZMOE_GROUPED_GEMV");
+    v = (e && atoi(e) == 0) ? 0 : 1;
+  }
+  return v == 1;
+}
+
 static bool use_grouped(const zmoe_layer_desc* d, int B) {
   return B >= grouped_min_b() && d->hidden % 128 == 0 && d->inter % 128 == 0 && d->n_experts <= 1024;
+}
+
+static SeqMode seq_mode(const zmoe_layer_desc* d, int B) {
+  const int64_t pairs = static_cast<int64_t>(B) * d->top_k;
+  const bool gemv_ok = gemv_enabled() && B >= kGroupedGemvMinB && d->n_experts <= 1024 &&
+                       pairs >= static_cast<int64_t>(kGroupedGemvRowsMin) * d->n_experts;
+  // the MFMA GEMM wins from 16 rows per expert, and below that too while its
+  // parameters fit the LDS cache (measured: Qwen3 B=32, 2 rows per expert,
+  // 157 us vs 170 us on the GEMV; DeepSeek-V3 B=64, hidden 7168, 3182 us vs
+  // 1846 us)
+  const bool cached = grouped_params_cached(d->quant_mode, true, d->hidden, d->group_size);
+  if (use_grouped(d, B) &&
+      (pairs >= static_cast<int64_t>(kGroupedMfmaRows) * d->n_experts || cached || !gemv_ok))
+    return kSeqMfma;
+  return gemv_ok ? kSeqGemv : kSeqPairs;
 }
 
 struct LayerWs {
@@ -65,11 +102,16 @@ static LayerWs layout_ws(const zmoe_layer_desc* d, int B, char* base) {
   ws.y = take(BK * d->hidden * 2);
   ws.sh_act = take(static_cast<size_t>(B) * (d->shared_inter > 0 ? d->shared_inter : 0) * 2);
   ws.sh_y = take(static_cast<size_t>(B) * (d->shared_inter > 0 ? d->hidden : 0) * 2);
-  if (use_grouped(d, B)) {
-    const int gs = d->group_size > 0 ? d->group_size : 32;
+  const SeqMode mode = seq_mode(d, B);
+  if (mode != kSeqPairs) {
+    const int nb = mode == kSeqMfma ? grouped_max_blocks(static_cast<int>(BK), d->n_experts)
+                                    : grouped_gemv_max_chunks(static_cast<int>(BK), d->n_experts);
     ws.offsets = static_cast<int*>(take(static_cast<size_t>(d->n_experts + 2) * 4));
     ws.sorted = static_cast<int*>(take(BK * 4));
-    ws.blocks = static_cast<int*>(take(static_cast<size_t>(grouped_max_blocks(static_cast<int>(BK), d->n_experts)) * 4));
+    ws.blocks = static_cast<int*>(take(static_cast<size_t>(nb) * 4));
+  }
+  if (mode == kSeqMfma) {
+    const int gs = d->group_size > 0 ? d->group_size : 32;
     ws.xsum = static_cast<float*>(take(static_cast<size_t>(B) * (d->hidden / gs) * 4));
     ws.asum = static_cast<float*>(take(BK * (d->inter / gs) * 4));
   }
@@ -190,7 +232,52 @@ extern "C" int zmoe_moe_layer(void* stream, const zmoe_layer_desc* d, const void
   }
   if (rc) return rc;
   // 3. routed experts: gate/up + SwiGLU, then down
-  if (use_grouped(d, B)) {
+  const SeqMode mode = seq_mode(d, B);
+  if (mode == kSeqGemv) {
+    // expert-major GEMV over the pairs sorted by expert; act and y stay in
+    // pair order
+    const int npairs = B * K;
+    rc = launch_sort_pairs(st, ws.idx, npairs, E, ws.offsets, ws.sorted, ws.blocks, kGroupedGemvRows);
+    if (rc) return rc;
+    GroupedArgs g{};
+    g.a = static_cast<const uint16_t*>(x);
+    g.lda = H;
+    g.offsets = ws.offsets;
+    g.blocks = ws.blocks;
+    g.E = E;
+    g.sorted = ws.sorted;
+    g.a_div = K;  // pair (b, k) reads token b
+    g.scatter = 1;
+    g.M = npairs;
+    g.w0 = d->gate_w;
+    g.s0 = d->gate_s;
+    g.b0 = d->gate_b;
+    g.w1 = d->up_w;
+    g.s1 = d->up_s;
+    g.b1 = d->up_b;
+    g.N = I;
+    g.K = H;
+    g.gs = d->group_size;
+    g.out = static_cast<uint16_t*>(ws.act);
+    g.ldo = I;
+    rc = launch_grouped_qmv(st, g, E, d->quant_mode, true);
+    if (rc) return rc;
+    g.a = static_cast<const uint16_t*>(ws.act);
+    g.lda = I;
+    g.a_div = 1;  // pair p reads act row p
+    g.w0 = d->down_w;
+    g.s0 = d->down_s;
+    g.b0 = d->down_b;
+    g.w1 = nullptr;
+    g.s1 = nullptr;
+    g.b1 = nullptr;
+    g.N = H;
+    g.K = I;
+    g.out = static_cast<uint16_t*>(ws.y);
+    g.ldo = H;
+    rc = launch_grouped_qmv(st, g, E, d->quant_mode, false);
+    if (rc) return rc;
+  } else if (mode == kSeqMfma) {
     // grouped GEMMs on MFMA over the (token, k) pairs sorted by expert; act
     // and y stay in pair order
     const int npairs = B * K;

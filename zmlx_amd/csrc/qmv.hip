@@ -10,6 +10,7 @@
 //   * the activation rows are staged once per workgroup in LDS in the
 //     pair-permuted layout the dot2 dequant trick needs (zmoe_common.h).
 #include "zmoe_common.h"
+#include "zmoe_grouped.h"
 #include "zmoe_host.h"
 
 namespace zmoe {
@@ -247,6 +248,123 @@ static int launch_qmv_l(hipStream_t st, int L, const void* x, const uint32_t* wg
     default:
       return fail(ZMOE_EUNSUPPORTED, "[gather_qmm] unsupported lane split");
   }
+}
+
+// ---------------------------------------------------------------------------
+// Expert-major GEMV over the expert-sorted (token, k) pairs: block (row tile,
+// chunk c) takes the chunk's expert e and its up to NT sorted rows, stages
+// those activation rows in LDS, and streams e's weight rows once for all of
+// them (wave_qmv, the same arithmetic as k_gather_qmv).  Results go to the
+// rows' pair positions (scatter) or their sorted positions.
+// ---------------------------------------------------------------------------
+constexpr int kGemvRows = 128;  // weight rows per workgroup of the expert-major GEMV
+
+template <int L, int J, int NT, int QMODE, bool SWIGLU>
+__global__ __launch_bounds__(kQmvThreads) void k_grouped_qmv(GroupedArgs g, int gshift, int tiles) {
+  extern __shared__ __align__(16) uint32_t smem[];
+  const int K = g.K, N = g.N;
+  const int S = K >> 5;
+  uint32_t* xs = smem;
+  float* sx = reinterpret_cast<float*>(smem + NT * S * 16);
+  const int c = blockIdx.y;
+  if (c >= g.offsets[g.E + 1]) return;  // whole workgroup: past the chunk list
+  const int ce = g.blocks[c];
+  const int64_t e = ce & 2047;
+  const int r_begin = g.offsets[e] + (ce >> 11) * NT;
+  const int ntok = min(NT, g.offsets[e + 1] - r_begin);
+  for (int t = 0; t < ntok; ++t) {
+    const int src = g.sorted[r_begin + t];
+    const int64_t arow = g.a_div > 0 ? src / g.a_div : src;
+    stage_x_row<QMODE>(g.a + arow * g.lda, S, xs, sx, t);
+  }
+  __syncthreads();
+  constexpr int RPW = J * (kWave / L);
+  const int wave = threadIdx.x / kWave;
+  const int64_t wstride = static_cast<int64_t>(N) * (K >> 3);
+  const int64_t pstride = static_cast<int64_t>(N) * ((QMODE == ZMOE_Q_AFFINE) ? (S >> gshift) : S);
+  const int pbytes = (QMODE == ZMOE_Q_AFFINE) ? 2 : 1;
+  const uint32_t* wg = g.w0 + e * wstride;
+  const void* sg = static_cast<const char*>(g.s0) + e * pstride * pbytes;
+  const void* bg = (QMODE == ZMOE_Q_AFFINE) ? static_cast<const void*>(static_cast<const char*>(g.b0) + e * pstride * 2)
+                                            : nullptr;
+  const uint32_t* wu = SWIGLU ? g.w1 + e * wstride : nullptr;
+  const void* su = SWIGLU ? static_cast<const void*>(static_cast<const char*>(g.s1) + e * pstride * pbytes) : nullptr;
+  const void* bu = (SWIGLU && QMODE == ZMOE_Q_AFFINE)
+                       ? static_cast<const void*>(static_cast<const char*>(g.b1) + e * pstride * 2)
+                       : nullptr;
+  // the block covers `tiles` consecutive row tiles (about kGemvRows rows) with
+  // one staging of the chunk's rows: the index loads and the staging are paid
+  // once for all of them
+  const int lane = threadIdx.x & (kWave - 1);
+  int64_t orow[NT];
+#pragma unroll
+  for (int tok = 0; tok < NT; ++tok)
+    orow[tok] = tok < ntok ? (g.scatter ? static_cast<int64_t>(g.sorted[r_begin + tok]) : r_begin + tok) : 0;
+  for (int tt = 0; tt < tiles; ++tt) {
+    const int row0 = ((blockIdx.x * tiles + tt) * kQmvWaves + wave) * RPW;
+    if (row0 >= N) break;
+    float rg[J][NT], ru[J][NT];
+    wave_qmv<L, J, NT, QMODE, SWIGLU>(wg, sg, bg, wu, su, bu, N, K, gshift, row0, ntok, xs, sx, rg, ru);
+    if ((lane % L) == 0) {
+      const int rs = lane / L;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const int r = row0 + j * (kWave / L) + rs;
+        if (r < N) {
+#pragma unroll
+          for (int tok = 0; tok < NT; ++tok) {
+            if (tok < ntok) {
+              const uint32_t v = SWIGLU ? swiglu_bf16(round_bf16(rg[j][tok]), round_bf16(ru[j][tok]))
+                                        : f32_to_bf16_bits(rg[j][tok]);
+              g.out[orow[tok] * g.ldo + r] = static_cast<uint16_t>(v);
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int L, int J, int QMODE, bool SWIGLU>
+static int launch_grouped_qmv_t(hipStream_t st, const GroupedArgs& g, int n_experts, int gshift) {
+  constexpr int NT = kGroupedGemvRows;
+  constexpr int RPW = J * (kWave / L);
+  const int S = g.K >> 5;
+  const int tiles = kGemvRows / (kQmvWaves * RPW) > 0 ? kGemvRows / (kQmvWaves * RPW) : 1;
+  const int rows_per_block = kQmvWaves * RPW * tiles;
+  dim3 grid((g.N + rows_per_block - 1) / rows_per_block, static_cast<unsigned>(grouped_gemv_max_chunks(g.M, n_experts)));
+  const size_t lds = static_cast<size_t>(NT) * S * 64 + static_cast<size_t>(NT) * S * 4;
+  hipLaunchKernelGGL((k_grouped_qmv<L, J, NT, QMODE, SWIGLU>), grid, dim3(kQmvThreads), lds, st, g, gshift, tiles);
+  return check_launch(SWIGLU ? "grouped gather_qmm_swiglu (gemv)" : "grouped gather_qmm (gemv)");
+}
+
+template <int QMODE, bool SWIGLU>
+static int launch_grouped_qmv_l(hipStream_t st, const GroupedArgs& g, int n_experts, int gshift) {
+  switch (gcd_int(g.K >> 5, kWave)) {
+    case 64:
+      return launch_grouped_qmv_t<64, 1, QMODE, SWIGLU>(st, g, n_experts, gshift);
+    case 32:
+      return launch_grouped_qmv_t<32, 1, QMODE, SWIGLU>(st, g, n_experts, gshift);
+    case 16:
+      return launch_grouped_qmv_t<16, 1, QMODE, SWIGLU>(st, g, n_experts, gshift);
+    case 8:
+      return launch_grouped_qmv_t<8, 1, QMODE, SWIGLU>(st, g, n_experts, gshift);
+    default:
+      return fail(ZMOE_EUNSUPPORTED, "[gather_qmm] unsupported lane split");
+  }
+}
+
+int launch_grouped_qmv(hipStream_t st, const GroupedArgs& g, int n_experts, int quant_mode, bool swiglu) {
+  if (g.M == 0) return ZMOE_OK;
+  ZMOE_REQUIRE(g.K % 256 == 0, ZMOE_EINVAL_SHAPE, "[gather_qmm] K must be a multiple of 256.");
+  int gshift = 0;
+  if (quant_mode == ZMOE_Q_AFFINE)
+    for (int v = g.gs / 32; v > 1; v >>= 1) ++gshift;
+  if (quant_mode == ZMOE_Q_AFFINE)
+    return swiglu ? launch_grouped_qmv_l<ZMOE_Q_AFFINE, true>(st, g, n_experts, gshift)
+                  : launch_grouped_qmv_l<ZMOE_Q_AFFINE, false>(st, g, n_experts, gshift);
+  return swiglu ? launch_grouped_qmv_l<ZMOE_Q_MXFP4, true>(st, g, n_experts, gshift)
+                : launch_grouped_qmv_l<ZMOE_Q_MXFP4, false>(st, g, n_experts, gshift);
 }
 
 // Shared argument validation of the two gather-QMM entry points.  Messages

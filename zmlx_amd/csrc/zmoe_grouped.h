@@ -33,11 +33,26 @@ struct GroupedArgs {
 // k_grouped_qmm over every expert's sorted rows; SwiGLU of two matrices when
 // swiglu (w1/s1/b1 = up), else one matrix.
 int launch_grouped(hipStream_t st, const GroupedArgs& g, int n_experts, int quant_mode, bool swiglu);
+// Whether the MFMA GEMM over K inputs keeps its scales/biases in the LDS
+// parameter cache (else it loads them per k block and runs slower).
+bool grouped_params_cached(int quant_mode, bool swiglu, int K, int gs);
 // offsets[E+2] / sorted[npairs]: the pairs (token, k) in expert order;
-// blocks[]: every expert's 64-row chunks (at most npairs / 64 + E of them).
-int launch_sort_pairs(hipStream_t st, const uint32_t* idx, int npairs, int E, int* offsets, int* sorted, int* blocks);
+// blocks[]: every expert's chunks of `chunk` rows (at most npairs / chunk + E
+// of them; 64 for the MFMA GEMM, kGroupedGemvRows for the GEMV).
+int launch_sort_pairs(hipStream_t st, const uint32_t* idx, int npairs, int E, int* offsets, int* sorted, int* blocks,
+                      int chunk = 64);
 // Upper bound on the 64-row chunks of npairs pairs over E experts.
 inline int grouped_max_blocks(int npairs, int E) { return (npairs + 63) / 64 + E; }
+
+// Expert-major GEMV (qmv.hip) for batches with few rows per expert: each
+// expert's weight rows are read once per chunk of kGroupedGemvRows sorted
+// rows and dotted with all of them (the same GroupedArgs; asum unused, the
+// chunk list from launch_sort_pairs(..., kGroupedGemvRows)).
+constexpr int kGroupedGemvRows = 4;
+inline int grouped_gemv_max_chunks(int npairs, int E) {
+  return (npairs + kGroupedGemvRows - 1) / kGroupedGemvRows + E;
+}
+int launch_grouped_qmv(hipStream_t st, const GroupedArgs& g, int n_experts, int quant_mode, bool swiglu);
 // out[r][g] = fp32 sum of a[r][g*gs .. +gs).
 int launch_row_group_sums(hipStream_t st, const uint16_t* a, int64_t lda, int rows, int K, int gs, float* out);
 
