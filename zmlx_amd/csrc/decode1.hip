@@ -244,8 +244,62 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
                           (rkind == kRouteSoftmaxProbs ||
                            (rkind == kRouteTopkLogits && p.route.bias == nullptr && p.route.norm));
   const int Epad = E <= 64 ? 64 : (E <= 128 ? 128 : 256);
+  // Routers that run route_row in wave 0 (grouped sigmoid, ...): with more
+  // than 64 experts every wave polls 64 experts' partials (summed in chunk
+  // order, rounded to bf16: the same logits), into L.keys, so the partials
+  // are read with 8 waves' loads in flight instead of one.
+  const bool par_poll = !rank_route && E > kWave && E <= kD1RankMaxE;
+  // the grouped router's bias, loaded before the logits are waited for
+  RowVals<P> biasv;
+  const bool pre_bias = !rank_route && rkind == kRouteSigmoidGrouped && p.route.bias != nullptr;
+  if (wave == 0 && pre_bias) {
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      const int e = lane + 64 * i;
+      biasv.v[i] = e < E ? gload(p.route.bias + e) : 0.0f;
+    }
+  }
+  if (par_poll) {
+    const int e = wave * kWave + lane;
+    if (wave * kWave < E) {
+      float a = 0.0f;
+      for (unsigned n = 0;; ++n) {
+        bool ok = true;
+        a = 0.0f;
+        if (e < E) {
+          unsigned long long part[kMaxNC];
+#pragma unroll
+          for (int c = 0; c < kMaxNC; ++c)
+            if (c < NC) part[c] = dev_load(p.rpart + static_cast<int64_t>(e) * NC + c);
+#pragma unroll
+          for (int c = 0; c < kMaxNC; ++c) {
+            if (c < NC) {
+              ok = ok && static_cast<unsigned>(part[c] >> 32) == tag;
+              a += __uint_as_float(static_cast<uint32_t>(part[c]));  // chunks in order
+            }
+          }
+        }
+        if (__all(ok)) break;
+        if (n > kSpinLimit) {
+          if (lane == 0) wait_timeout(p);
+          break;
+        }
+      }
+      if (e < E) L.keys[e] = __float_as_uint(round_bf16(a));
+    }
+    lds_barrier();
+  }
   if (wave == 0) {
-    RowVals<P> row = poll_logits<P>(p, p.rpart, NC, tag);
+    RowVals<P> row;
+    if (par_poll) {
+#pragma unroll
+      for (int i = 0; i < P; ++i) {
+        const int e = lane + 64 * i;
+        row.v[i] = e < E ? __uint_as_float(L.keys[e]) : -INFINITY;
+      }
+    } else {
+      row = poll_logits<P>(p, p.rpart, NC, tag);
+    }
     trace_mark(p, 3);
     if (rank_route) {
       float(&v)[P] = row.v;
@@ -266,7 +320,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
       }
       trace_mark(p, 15);
     } else {
-      route_row<P>(p.route, row, *(ZMOE_LDS RouteLds*)(&L.route), (ZMOE_LDS float*)grow);
+      route_row<P>(p.route, row, *(ZMOE_LDS RouteLds*)(&L.route), (ZMOE_LDS float*)grow, pre_bias ? &biasv : nullptr);
       if (lane < Uall * 3) set_unit_e(p, L, lane / 3, lane % 3, lane / 3 < K ? L.route.sel[lane / 3] : -1);
       if (blockIdx.x == 0 && lane < K) {
         if (p.out_idx) gstore(p.out_idx + lane, static_cast<uint32_t>(L.route.sel[lane]));

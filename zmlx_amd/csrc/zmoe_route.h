@@ -229,8 +229,27 @@ struct RowVals {
 // Routes one row of logits given lane-strided in row.v (entries >= E
 // ignored).  Results: R.sel[0..k), R.w[0..k).  All 64 lanes call it.
 // `grow` is E floats of wave-private LDS (grouped router only).
+// Top-2 of the 32 values held by a 32-lane half of the wave (lanes h*32 ..
+// h*32+31), returned to every lane of the half: butterfly merges of
+// (first, second) pairs.  max/min of floats are exact, so the pair equals
+// the serial scan's.
+__device__ __forceinline__ void half_top2(float x, float& t1, float& t2) {
+  t1 = x;
+  t2 = -INFINITY;
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1) {
+    const float b1 = __shfl_xor(t1, o), b2 = __shfl_xor(t2, o);
+    const float n2 = fmaxf(fminf(t1, b1), fmaxf(t2, b2));
+    t1 = fmaxf(t1, b1);
+    t2 = n2;
+  }
+}
+
+// `bias_pre` (optional): the bias values bias[lane + 64 i], loaded by the
+// caller ahead of time (grouped router), so route_row does not wait for them.
 template <int P>
-__device__ __forceinline__ void route_row(const RouteArgs a, RowVals<P> row, ZMOE_LDS RouteLds& R, ZMOE_LDS float* grow) {
+__device__ __forceinline__ void route_row(const RouteArgs a, RowVals<P> row, ZMOE_LDS RouteLds& R, ZMOE_LDS float* grow,
+                                          const RowVals<P>* bias_pre = nullptr) {
   float (&v)[P] = row.v;
   const int lane = __lane_id();
   const int E = a.E, k = a.k;
@@ -280,10 +299,19 @@ __device__ __forceinline__ void route_row(const RouteArgs a, RowVals<P> row, ZMO
     for (int i = 0; i < P; ++i) {
       const int e = lane + 64 * i;
       aux[i] = sigmoid_abs(v[i]);
-      v[i] = aux[i] + (e < E ? gload(a.bias + e) : 0.0f);
+      v[i] = aux[i] + (e < E ? (bias_pre ? bias_pre->v[i] : gload(a.bias + e)) : 0.0f);
     }
     if (a.n_group > 1 && a.topk_group < a.n_group) {
       const int gsz = E / a.n_group, ng = a.n_group, kg = a.topk_group;
+      if (gsz == 32 && E == 64 * P) {
+        // group g = register g / 2, lane half g % 2: a 32-lane top-2 each
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+          float t1, t2;
+          half_top2(v[i], t1, t2);
+          if ((lane & 31) == 0) R.gsc[2 * i + (lane >> 5)] = t1 + t2;
+        }
+      } else {
 #pragma unroll
       for (int i = 0; i < P; ++i)
         if (lane + 64 * i < E) grow[lane + 64 * i] = v[i];
@@ -301,6 +329,7 @@ __device__ __forceinline__ void route_row(const RouteArgs a, RowVals<P> row, ZMO
           }
         }
         R.gsc[lane] = t1 + t2;
+      }
       }
       wave_lds_sync();
       // keep the topk_group best groups (ties -> lower group index)
