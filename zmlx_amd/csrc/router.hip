@@ -14,7 +14,7 @@ constexpr int kRouterMaxK = kMaxTopK;
 // Dense router projection: logits[b, e] = x[b, :] . w[e, :]
 // ---------------------------------------------------------------------------
 constexpr int kLogitTok = 4;   // tokens per block
-constexpr int kLogitRows = 2;  // rows per wave
+constexpr int kLogitRows = 1;  // rows per wave (short dependent chains: one row of wave sums per wave)
 
 __global__ __launch_bounds__(256) void k_dense_logits(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                                       int B, int E, int H, int out_f32, void* __restrict__ out) {
