@@ -19,7 +19,7 @@ torch = pytest.importorskip("torch")
 transformers = pytest.importorskip("transformers")
 
 from zmlx_amd import patch as P  # noqa: E402
-from zmlx_amd.quant import dequantize, quantize_affine  # noqa: E402
+from zmlx_amd.quant import dequantize, quantize_affine, quantize_mxfp4  # noqa: E402
 
 H, I, E, K = 512, 256, 16, 4
 
@@ -58,21 +58,28 @@ def _init_block(block, std=0.05):
             block.gate.e_score_correction_bias.normal_(0.0, 0.05)
 
 
-def _dequantise_experts_(block, gs=64):
-    """Replace the block's expert weights by their affine-4-bit round trip
-    and its router weight by its bf16 rounding (the kernels' operands)."""
+def _roundtrip(w, gs, mode):
+    if mode == "mxfp4":
+        q, s = quantize_mxfp4(w)
+        return dequantize(q, s, None, mode="mxfp4")
+    q, s, b = quantize_affine(w, gs)
+    return dequantize(q, s, b, group_size=gs)
+
+
+def _dequantise_experts_(block, gs=64, mode="affine"):
+    """Replace the block's expert weights by their 4-bit round trip (affine
+    or mxfp4) and its router weight by its bf16 rounding (the kernels'
+    operands)."""
     with torch.no_grad():
         block.gate.weight.copy_(block.gate.weight.to(torch.bfloat16).float())
         for name in ("gate_up_proj", "down_proj"):
             w = getattr(block.experts, name)
-            q, s, b = quantize_affine(w.detach().float(), gs)
-            w.copy_(dequantize(q, s, b, group_size=gs))
+            w.copy_(_roundtrip(w.detach().float(), gs, mode))
         sh = getattr(block, "shared_experts", None)
         if sh is not None:
             for n in ("gate_proj", "up_proj", "down_proj"):
                 w = getattr(sh, n).weight
-                q, s, b = quantize_affine(w.detach().float(), gs)
-                w.copy_(dequantize(q, s, b, group_size=gs))
+                w.copy_(_roundtrip(w.detach().float(), gs, mode))
 
 
 # ---------------------------------------------------------------------------
@@ -238,14 +245,17 @@ def test_patched_qwen3_block_matches_transformers(dev, B):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["affine", "mxfp4"])
 @pytest.mark.parametrize("B", [1, 6])
-def test_patched_deepseek_block_matches_transformers(dev, B):
+def test_patched_deepseek_block_matches_transformers(dev, B, mode):
     blk = _deepseek_block()
     _init_block(blk)
     blk = blk.to(dev)
     ref_blk = copy.deepcopy(blk)
-    _dequantise_experts_(ref_blk)
-    P.patch(blk)
+    _dequantise_experts_(ref_blk, mode=mode)
+    P.patch(blk, quant_mode=mode)
+    res = blk._zmlx_patch_result
+    assert res.patched_count == 1, res.summary()
     g = torch.Generator(device=dev).manual_seed(10 + B)
     x = torch.randn(1, B, H, device=dev, generator=g).to(torch.bfloat16).float()
     with torch.no_grad():
