@@ -251,6 +251,9 @@ FUSED_CASES = [
     ("lfm2", dict(H=2048, E=32, I=1792, K=4), [1, 3, 16]),
     ("glm", dict(H=2048, E=64, I=1536, K=4, mode="mxfp4", gs=32, shared_I=1536), [1, 8, 16, 2]),
     ("deepseek", dict(H=1024, E=256, I=512, K=8, shared_I=512), [1, 2]),
+    # hidden sizes other than 2048 take the one-token kernel's general path
+    ("glm_h3072", dict(H=3072, E=64, I=1024, K=4, mode="mxfp4", gs=32, shared_I=1024), [1]),
+    ("qwen3_h4096", dict(H=4096, E=64, I=1536, K=8), [1]),
 ]
 
 
@@ -263,6 +266,7 @@ def test_single_launch_matches_kernel_sequence(dev, family, shape, batches):
 
     rng = np.random.default_rng(17)
     kw = {}
+    family = family.split("_")[0]
     if family in ("glm", "deepseek"):
         kw["router_bias"] = (rng.standard_normal(shape["E"]) * 0.05).astype(np.float32)
         kw["routed_scaling_factor"] = 2.5

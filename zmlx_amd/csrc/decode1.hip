@@ -25,6 +25,8 @@
 // keeps the kernel within the scalar register file (no spills).
 #include "zmoe_fused.h"
 
+#include <type_traits>
+
 namespace zmoe {
 
 constexpr int kD1MaxUnits = kMaxTopK + 1;
@@ -357,27 +359,35 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
   // ---------------- D setup: this wave's down-projection loads ----------------
   const int64_t wprD = I >> 3;
   const int64_t pprD = (QMODE == ZMOE_Q_AFFINE) ? (S_I >> p.gshift) : S_I;
-  uint4 wd[kD1D];
-  RawParam rd[kD1D];
-  int jhl[kD1D], ju[kD1D], jt[kD1D];
-  bool jvalid[kD1D];
+  // Hidden 2048 (XR) fits a wave's down items in one batch.  Other shapes
+  // keep two batches in registers, both loaded with the gate/up rows; the D
+  // loop refills each batch once it is computed, so one is in flight while
+  // the other is computed.
+  constexpr int DB = XR ? 1 : 2;
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  uint4 wd[DB][kD1D];
+  RawParam rd[DB][kD1D];
+  int jhl[DB][kD1D], ju[DB][kD1D], jt[DB][kD1D];
+  bool jvalid[DB][kD1D];
   // Loads are unconditional so that waits count them: items past the end
   // repeat the previous item's address (a cache hit), or read x if the wave
   // has no down work.
-  auto load_down = [&](int base) {
+  auto load_down = [&](int base, auto bc) {
+    constexpr int b = decltype(bc)::value;
     const uint32_t* wp = reinterpret_cast<const uint32_t*>(p.x);
     const void* sp = p.x;
     const void* bp = p.x;
     int64_t poff = 0;
 #pragma unroll
     for (int j = 0; j < kD1D; ++j) {
-      jhl[j] = min(d_hl, max(nrows - 1, 0));
-      ju[j] = d_u;
-      jt[j] = d_t;
-      jvalid[j] = d_g * RPID + rsD < slots;
+      jhl[b][j] = min(d_hl, max(nrows - 1, 0));
+      ju[b][j] = d_u;
+      jt[b][j] = d_t;
+      jvalid[b][j] = d_g * RPID + rsD < slots;
       if (base + j < n_itemsD) {
         const int s = d_t * LI + liD;
-        const int64_t row = h0 + jhl[j];
+        const int64_t row = h0 + jhl[b][j];
         wp = L.w[2][d_u] + row * wprD + s * 4;
         sp = L.s[2][d_u];
         bp = L.b[2][d_u];
@@ -392,8 +402,8 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
           d_u = (d_hl >= nrows) ? 0 : d_u;
         }
       }
-      wd[j] = gload(reinterpret_cast<const uint4*>(wp));
-      rd[j] = seg_param_load<QMODE>(sp, bp, poff);
+      wd[b][j] = gload(reinterpret_cast<const uint4*>(wp));
+      rd[b][j] = seg_param_load<QMODE>(sp, bp, poff);
     }
   };
 
@@ -448,7 +458,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
     // gate/up loads first, then the down loads: loads return in order, so
     // the gate/up rows are computed while the down bytes still stream
     if (g0 < g1) load_a(g0);
-    load_down(0);
+    load_down(0, B0{});
     if (rank_route && wave == 0) rank_weights(p, L, K);
     for (int base = g0; base < g1; base += kD1A) {
       if (base != g0) load_a(base);
@@ -491,23 +501,33 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
     int cu = a_cu;
     int crg = a_cr;
     int ct = 0;
-    uint4 wg[kD1A], wu[kD1A];
-    RawParam rg[kD1A], ru[kD1A];
-    int iu[kD1A], irow[kD1A], it_[kD1A];
-    auto load_a = [&](int base) {
+    // two batches of items in registers: one in flight while the other is
+    // computed; loads are unconditional (items past the end repeat the
+    // previous item's address, or read x if the wave has no items)
+    uint4 wg[2][kD1A], wu[2][kD1A];
+    RawParam rg[2][kD1A], ru[2][kD1A];
+    int iu[2][kD1A], irow[2][kD1A], it_[2][kD1A];
+    auto load_a = [&](int base, auto bc) {
+      constexpr int b = decltype(bc)::value;
+      const uint32_t* gwp = reinterpret_cast<const uint32_t*>(p.x);
+      const uint32_t* uwp = gwp;
+      const void *gsp = p.x, *gbp = p.x, *usp = p.x, *ubp = p.x;
+      int64_t poff = 0;
 #pragma unroll
       for (int j = 0; j < kD1A; ++j) {
-        iu[j] = cu;
-        irow[j] = crg * RPI + rs;
-        it_[j] = ct;
+        iu[b][j] = cu;
+        irow[b][j] = crg * RPI + rs;
+        it_[b][j] = ct;
         if (base + j < n_items) {
           const int s = ct * LH + li;
-          const int64_t row = irow[j];
-          wg[j] = gload(reinterpret_cast<const uint4*>(L.w[0][cu] + row * wpr + s * 4));
-          wu[j] = gload(reinterpret_cast<const uint4*>(L.w[1][cu] + row * wpr + s * 4));
-          const int pi = (QMODE == ZMOE_Q_AFFINE) ? (s >> p.gshift) : s;
-          rg[j] = seg_param_load<QMODE>(L.s[0][cu], L.b[0][cu], row * ppr + pi);
-          ru[j] = seg_param_load<QMODE>(L.s[1][cu], L.b[1][cu], row * ppr + pi);
+          const int64_t row = irow[b][j];
+          gwp = L.w[0][cu] + row * wpr + s * 4;
+          uwp = L.w[1][cu] + row * wpr + s * 4;
+          gsp = L.s[0][cu];
+          gbp = L.b[0][cu];
+          usp = L.s[1][cu];
+          ubp = L.b[1][cu];
+          poff = row * ppr + ((QMODE == ZMOE_Q_AFFINE) ? (s >> p.gshift) : s);
           if (++ct == T) {
             ct = 0;
             if (++crg == rgu) {
@@ -516,35 +536,48 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
             }
           }
         }
+        wg[b][j] = gload(reinterpret_cast<const uint4*>(gwp));
+        wu[b][j] = gload(reinterpret_cast<const uint4*>(uwp));
+        rg[b][j] = seg_param_load<QMODE>(gsp, gbp, poff);
+        ru[b][j] = seg_param_load<QMODE>(usp, ubp, poff);
       }
     };
-    if (n_items > 0) load_a(0);
-    load_down(0);
-    if (rank_route && wave == 0) rank_weights(p, L, K);
     float ag = 0.0f, au = 0.0f;
-    for (int base = 0; base < n_items; base += kD1A) {
-      if (base > 0) load_a(base);
+    auto compute_a = [&](int base, auto bc) {
+      constexpr int b = decltype(bc)::value;
 #pragma unroll
       for (int j = 0; j < kD1A; ++j) {
         if (base + j < n_items) {
-          const int t = it_[j];
+          const int t = it_[b][j];
           const int s = t * LH + li;
           float sgj, cgj, suj, cuj;
-          seg_param_decode<QMODE>(rg[j], sgj, cgj);
-          seg_param_decode<QMODE>(ru[j], suj, cuj);
+          seg_param_decode<QMODE>(rg[b][j], sgj, cgj);
+          seg_param_decode<QMODE>(ru[b][j], suj, cuj);
           const float xsum = (QMODE == ZMOE_Q_AFFINE) ? sx[s] : 0.0f;
-          ag = seg_accum<QMODE>(t == 0 ? 0.0f : ag, sgj, cgj, seg_dot_lds<QMODE>(wg[j], xs, S_H, 0, s, ak), xsum);
-          au = seg_accum<QMODE>(t == 0 ? 0.0f : au, suj, cuj, seg_dot_lds<QMODE>(wu[j], xs, S_H, 0, s, ak), xsum);
+          ag = seg_accum<QMODE>(t == 0 ? 0.0f : ag, sgj, cgj, seg_dot_lds<QMODE>(wg[b][j], xs, S_H, 0, s, ak), xsum);
+          au = seg_accum<QMODE>(t == 0 ? 0.0f : au, suj, cuj, seg_dot_lds<QMODE>(wu[b][j], xs, S_H, 0, s, ak), xsum);
           if (base == 0 && j == 0) trace_mark(p, 6);
           if (t == T - 1) {
             const float gv = lanes_sum(ag, LH);
             const float uv = lanes_sum(au, LH);
             if (li == 0)
-              dev_store(p.act + static_cast<int64_t>(iu[j]) * p.act_stride + irow[j],
+              dev_store(p.act + static_cast<int64_t>(iu[b][j]) * p.act_stride + irow[b][j],
                         (tag16 << 16) | swiglu_bf16(round_bf16(gv), round_bf16(uv)));
           }
         }
       }
+    };
+    // gate/up loads first, then the down loads (loads return in order)
+    load_a(0, B0{});
+    load_a(kD1A, B1{});
+    load_down(0, B0{});
+    load_down(kD1D, B1{});
+    if (rank_route && wave == 0) rank_weights(p, L, K);
+    for (int base = 0; base < n_items; base += 2 * kD1A) {
+      compute_a(base, B0{});
+      load_a(base + 2 * kD1A, B0{});
+      compute_a(base + kD1A, B1{});
+      load_a(base + 3 * kD1A, B1{});
     }
   }
   trace_mark(p, 7);
@@ -583,23 +616,49 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
   lds_barrier();
   trace_mark(p, 10);
   float acc = 0.0f;
-  for (int base = 0; base < n_itemsD; base += kD1D) {
-    if (base > 0) load_down(base);
+  // The lane-group width of the row sums is a template constant of the loop
+  // (a runtime width costs a branch tree per item).
+  auto compute_d = [&](int base, auto bc, auto lic) {
+    constexpr int b = decltype(bc)::value;
+    constexpr int LIc = decltype(lic)::value;
 #pragma unroll
     for (int j = 0; j < kD1D; ++j) {
       if (base + j < n_itemsD) {
-        const int u = ju[j], t = jt[j];
-        const int s = t * LI + liD;
+        const int u = ju[b][j], t = jt[b][j];
+        const int s = t * LIc + liD;
         float sdj, cdj;
-        seg_param_decode<QMODE>(rd[j], sdj, cdj);
+        seg_param_decode<QMODE>(rd[b][j], sdj, cdj);
         const float xsum = (QMODE == ZMOE_Q_AFFINE) ? asx[u * S_I + s] : 0.0f;
-        acc = seg_accum<QMODE>(t == 0 ? 0.0f : acc, sdj, cdj, seg_dot_lds<QMODE>(wd[j], as, S_I, u, s, ak), xsum);
+        acc = seg_accum<QMODE>(t == 0 ? 0.0f : acc, sdj, cdj, seg_dot_lds<QMODE>(wd[b][j], as, S_I, u, s, ak), xsum);
         if (t == TD - 1) {
-          const float y = lanes_sum(acc, LI);
-          if (liD == 0 && jvalid[j]) ybuf[(wave * rpw + jhl[j]) * Uall + u] = round_bf16(y);
+          const float y = wave_sum_width<LIc>(acc);
+          if (liD == 0 && jvalid[b][j]) ybuf[(wave * rpw + jhl[b][j]) * Uall + u] = round_bf16(y);
         }
       }
     }
+  };
+  auto d_loop = [&](auto lic) {
+    if constexpr (XR) {
+      for (int base = 0; base < n_itemsD; base += kD1D) {
+        if (base > 0) load_down(base, B0{});
+        compute_d(base, B0{}, lic);
+      }
+    } else {
+      for (int base = 0; base < n_itemsD; base += 2 * kD1D) {
+        compute_d(base, B0{}, lic);
+        load_down(base + 2 * kD1D, B0{});
+        compute_d(base + kD1D, B1{}, lic);
+        load_down(base + 3 * kD1D, B1{});
+      }
+    }
+  };
+  switch (LI) {  // LI = gcd(I / 32, 64), as lanes_sum
+    case 64: d_loop(std::integral_constant<int, 64>{}); break;
+    case 32: d_loop(std::integral_constant<int, 32>{}); break;
+    case 16: d_loop(std::integral_constant<int, 16>{}); break;
+    case 8: d_loop(std::integral_constant<int, 8>{}); break;
+    case 4: d_loop(std::integral_constant<int, 4>{}); break;
+    default: d_loop(std::integral_constant<int, 2>{});
   }
   wave_lds_sync();
   trace_mark(p, 11);
