@@ -283,3 +283,29 @@ def test_single_launch_matches_kernel_sequence(dev, family, shape, batches):
             np.testing.assert_array_equal(from_dev(w_f), from_dev(w_m))
             np.testing.assert_array_equal(from_dev(of), from_dev(om))
     assert fused.sync_error() == 0
+
+
+@pytest.mark.parametrize("family,shape,groups", [
+    ("deepseek", dict(H=1024, E=256, I=512, K=8, shared_I=512), dict(n_group=8, topk_group=4)),
+    ("glm", dict(H=2048, E=64, I=1536, K=4, mode="mxfp4", gs=32, shared_I=1536), {}),
+])
+def test_single_launch_routing_ties(dev, family, shape, groups):
+    """Grouped sigmoid routing with tied scores (zero input, bias on a coarse
+    grid): the single-launch kernel ranks fp32 keys with ties to the lower
+    index and keeps the same groups as the argmax rounds of the kernel
+    sequence; routing and outputs bit-identical."""
+    import torch
+
+    rng = np.random.default_rng(23)
+    bias = (rng.integers(-2, 3, shape["E"]) * 0.25).astype(np.float32)
+    fused, multi = _layer_pair(dev, rng, family, **shape, router_bias=bias, routed_scaling_factor=2.5, **groups)
+    xs = [np.zeros((1, shape["H"]), np.float32), bf16_randn(rng, (1, shape["H"]))]
+    for x in xs:
+        xt = to_bf16(x, dev)
+        of, i_f, w_f = fused(xt, return_routing=True)
+        om, i_m, w_m = multi(xt, return_routing=True)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(from_dev(i_f), from_dev(i_m))
+        np.testing.assert_array_equal(from_dev(w_f), from_dev(w_m))
+        np.testing.assert_array_equal(from_dev(of), from_dev(om))
+    assert fused.sync_error() == 0

@@ -25,6 +25,7 @@
 // keeps the kernel within the scalar register file (no spills).
 #include "zmoe_fused.h"
 
+#include <cstddef>
 #include <type_traits>
 
 namespace zmoe {
@@ -43,11 +44,14 @@ constexpr int kD1RankMaxE = 256;  // parallel ranking for E <= this
 
 struct D1Lds {
   RouteLds route;
-  uint32_t keys[kD1RankMaxE];         // packed (bf16 order key << 16 | 0xFFFF - e)
+  // packed (bf16 order key << 16 | 0xFFFF - e); the grouped sigmoid
+  // router's 64-bit keys use all of it
+  uint32_t keys[2 * kD1RankMaxE];
   const uint32_t* w[3][kD1MaxUnits];  // matrix (gate, up, down) x unit
   const void* s[3][kD1MaxUnits];
   const void* b[3][kD1MaxUnits];
 };
+static_assert(offsetof(D1Lds, keys) % 16 == 0, "keys are read as 16-byte vectors");
 
 struct D1Layout {
   size_t xs, sx, as, asx, ybuf, grow, total;
@@ -116,6 +120,98 @@ __device__ __forceinline__ int rank_in_row(const uint32_t* keys, int& i, uint32_
   if (Q >= 4) cnt += __builtin_amdgcn_update_dpp(0, cnt, kDppQuadSwap2, 0xF, 0xF, false);
   if (Q >= 8) cnt += __builtin_amdgcn_update_dpp(0, cnt, kDppHalfMirror, 0xF, 0xF, false);
   return q == 0 ? cnt : -1;
+}
+
+// Rank of 64-bit key i (number of larger keys; keys are unique) over an
+// EPAD-entry row, Q = 512/EPAD adjacent threads per key, each counting one
+// slice in chunks of up to 16 keys.  Returns the rank in thread q == 0 of each
+// group (-1 elsewhere).
+template <int EPAD>
+__device__ __forceinline__ int rank_in_row64(const uint64_t* keys, int& i, uint64_t& ki) {
+  constexpr int Q = kFThreads / EPAD;
+  constexpr int PER = EPAD / Q;
+  constexpr int CH = PER < 16 ? PER : 16;  // keys per chunk
+  static_assert(Q >= 2 && Q <= 8 && PER % CH == 0 && CH % 2 == 0, "rank slices");
+  i = threadIdx.x / Q;
+  const int q = threadIdx.x % Q;
+  ki = keys[i];
+  int cnt = 0;
+  for (int c = 0; c < PER; c += CH) {
+    uint4 kk[CH / 2];
+#pragma unroll
+    for (int m = 0; m < CH / 2; ++m) kk[m] = *reinterpret_cast<const uint4*>(&keys[q * PER + c + 2 * m]);
+#pragma unroll
+    for (int m = 0; m < CH / 2; ++m) {
+      cnt += ((static_cast<uint64_t>(kk[m].y) << 32 | kk[m].x) > ki) ? 1 : 0;
+      cnt += ((static_cast<uint64_t>(kk[m].w) << 32 | kk[m].z) > ki) ? 1 : 0;
+    }
+  }
+  cnt += __builtin_amdgcn_update_dpp(0, cnt, kDppQuadSwap1, 0xF, 0xF, false);
+  if (Q >= 4) cnt += __builtin_amdgcn_update_dpp(0, cnt, kDppQuadSwap2, 0xF, 0xF, false);
+  if (Q >= 8) cnt += __builtin_amdgcn_update_dpp(0, cnt, kDppHalfMirror, 0xF, 0xF, false);
+  return q == 0 ? cnt : -1;
+}
+
+// Grouped sigmoid router (moe.py:1501-1742, deepseek_router.py:118) for
+// E = 64 P experts, groups of 32 (or no group limit), wave 0: the selection
+// scores sigmoid + bias with the dropped groups' scores set to 0, as unique
+// keys (order key << 32 | ~e: value descending, then lower index) in
+// keys[e], and the sigmoids in aux[e].  The group top-2 sums are
+// 32-lane butterflies; the kept groups are the topk_group best by rank
+// (ties to the lower group), the set the argmax rounds of route_row keep.
+template <int P>
+__device__ __forceinline__ void sig_scores(const RouteArgs& a, RowVals<P> row, const RowVals<P>* bias_pre,
+                                           ZMOE_LDS RouteLds& R, uint64_t* keys, float* aux) {
+  const int lane = __lane_id();
+  float v[P], sg[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    sg[i] = sigmoid_abs(row.v[i]);
+    v[i] = sg[i] + (bias_pre ? bias_pre->v[i] : 0.0f);
+  }
+  if (a.n_group > 1 && a.topk_group < a.n_group) {
+    const int ng = a.n_group;
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      float t1, t2;
+      half_top2(v[i], t1, t2);
+      if ((lane & 31) == 0) R.gsc[2 * i + (lane >> 5)] = t1 + t2;
+    }
+    wave_lds_sync();
+    const uint32_t gk = lane < ng ? order_key(R.gsc[lane]) : 0u;
+    int rank = 0;
+    for (int g = 0; g < ng; ++g) {
+      const uint32_t o = order_key(R.gsc[g]);
+      rank += (o > gk || (o == gk && g < lane)) ? 1 : 0;
+    }
+    const uint64_t keepm = __ballot(lane < ng && rank < a.topk_group);
+#pragma unroll
+    for (int i = 0; i < P; ++i)
+      if (!((keepm >> ((lane + 64 * i) >> 5)) & 1ull)) v[i] = 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    keys[lane + 64 * i] = static_cast<uint64_t>(order_key(v[i])) << 32 | (0xFFFFFFFFu - static_cast<uint32_t>(lane + 64 * i));
+    aux[lane + 64 * i] = sg[i];
+  }
+}
+
+// Weights of the grouped sigmoid router's ranked winners (wave 0; lane r < K
+// holds winner r): the sigmoids normalised in selection order, scaled; then
+// the routing outputs of workgroup 0.
+__device__ __forceinline__ void sig_weights(const FusedParams& p, D1Lds& L, int K) {
+  const int lane = __lane_id();
+  const float a = lane < K ? L.route.saux[lane] : 0.0f;
+  const float sum = ordered_lane_sum(a, K);
+  float x = a / sum;
+  if (p.route.scale != 1.0f) x = x * p.route.scale;
+  if (lane < K) {
+    L.route.w[lane] = x;
+    if (blockIdx.x == 0) {
+      if (p.out_idx) gstore(p.out_idx + lane, static_cast<uint32_t>(L.route.sel[lane]));
+      if (p.out_w) gstore(p.out_w + lane, x);
+    }
+  }
 }
 
 // Gate weights of the ranked winners (wave 0; lane r < K holds winner r),
@@ -251,9 +347,16 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
   // order, rounded to bf16: the same logits), into L.keys, so the partials
   // are read with 8 waves' loads in flight instead of one.
   const bool par_poll = !rank_route && E > kWave && E <= kD1RankMaxE;
+  // Grouped sigmoid routers with E = 64 P experts and groups of 32 (or no
+  // group limit) also select by ranking, over fp32 score keys with index
+  // ties; the others run route_row in wave 0.
+  const bool sig_rank = !rank_route && rkind == kRouteSigmoidGrouped && E == kWave * P && K <= kMaxTopK &&
+                        (p.route.n_group <= 1 || p.route.topk_group >= p.route.n_group ||
+                         (p.route.n_group <= 64 && E == 32 * p.route.n_group));
   // the grouped router's bias, loaded before the logits are waited for
   RowVals<P> biasv;
   const bool pre_bias = !rank_route && rkind == kRouteSigmoidGrouped && p.route.bias != nullptr;
+  // (a null bias is zero only on the ranking path; route_row requires one)
   if (wave == 0 && pre_bias) {
 #pragma unroll
     for (int i = 0; i < P; ++i) {
@@ -321,6 +424,9 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
           L.keys[e] = e < E ? ((order_key(v[i]) & 0xFFFF0000u) | (0xFFFFu - static_cast<uint32_t>(e))) : 0u;
       }
       trace_mark(p, 15);
+    } else if (sig_rank) {
+      sig_scores<P>(p.route, row, pre_bias ? &biasv : nullptr, *(ZMOE_LDS RouteLds*)(&L.route),
+                    reinterpret_cast<uint64_t*>(L.keys), grow);
     } else {
       route_row<P>(p.route, row, *(ZMOE_LDS RouteLds*)(&L.route), (ZMOE_LDS float*)grow, pre_bias ? &biasv : nullptr);
       if (lane < Uall * 3) set_unit_e(p, L, lane / 3, lane % 3, lane / 3 < K ? L.route.sel[lane / 3] : -1);
@@ -351,6 +457,25 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
       for (int m = 0; m < 3; ++m) set_unit_e(p, L, K, m, -1);
     }
     trace_mark(p, 17);
+  } else if (sig_rank) {
+    int i, r;
+    uint64_t kl;
+    const uint64_t* k64 = reinterpret_cast<const uint64_t*>(L.keys);
+    if (Epad == 64) r = rank_in_row64<64>(k64, i, kl);
+    else if (Epad == 128) r = rank_in_row64<128>(k64, i, kl);
+    else r = rank_in_row64<256>(k64, i, kl);
+    if (r >= 0 && r < K) {
+      const uint32_t ki = static_cast<uint32_t>(kl >> 32);
+      L.route.sel[r] = i;
+      L.route.sval[r] = __uint_as_float((ki & 0x80000000u) ? (ki & 0x7FFFFFFFu) : ~ki);
+      L.route.saux[r] = grow[i];
+#pragma unroll
+      for (int m = 0; m < 3; ++m) set_unit_e(p, L, r, m, i);
+    }
+    if (has_shared && threadIdx.x == kFThreads - 1) {
+#pragma unroll
+      for (int m = 0; m < 3; ++m) set_unit_e(p, L, K, m, -1);
+    }
   }
   trace_mark(p, 4);
   lds_barrier();
@@ -460,6 +585,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
     if (g0 < g1) load_a(g0);
     load_down(0, B0{});
     if (rank_route && wave == 0) rank_weights(p, L, K);
+    if (sig_rank && wave == 0) sig_weights(p, L, K);
     for (int base = g0; base < g1; base += kD1A) {
       if (base != g0) load_a(base);
       float gv[kD1A], uv[kD1A];
@@ -573,12 +699,19 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
     load_down(0, B0{});
     load_down(kD1D, B1{});
     if (rank_route && wave == 0) rank_weights(p, L, K);
-    for (int base = 0; base < n_items; base += 2 * kD1A) {
+    if (sig_rank && wave == 0) sig_weights(p, L, K);
+    // while another pair of batches follows, compute one and refill it; the
+    // last one or two batches are computed without loads behind them, so the
+    // act stores are not left waiting on loads past the end
+    int base = 0;
+    for (; base + 2 * kD1A < n_items; base += 2 * kD1A) {
       compute_a(base, B0{});
       load_a(base + 2 * kD1A, B0{});
       compute_a(base + kD1A, B1{});
       load_a(base + 3 * kD1A, B1{});
     }
+    compute_a(base, B0{});
+    compute_a(base + kD1A, B1{});
   }
   trace_mark(p, 7);
   // All act rows of the grid are stored once every workgroup has arrived:
@@ -644,12 +777,15 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
         compute_d(base, B0{}, lic);
       }
     } else {
-      for (int base = 0; base < n_itemsD; base += 2 * kD1D) {
+      int base = 0;
+      for (; base + 2 * kD1D < n_itemsD; base += 2 * kD1D) {
         compute_d(base, B0{}, lic);
         load_down(base + 2 * kD1D, B0{});
         compute_d(base + kD1D, B1{}, lic);
         load_down(base + 3 * kD1D, B1{});
       }
+      compute_d(base, B0{}, lic);
+      compute_d(base + kD1D, B1{}, lic);
     }
   };
   switch (LI) {  // LI = gcd(I / 32, 64), as lanes_sum
