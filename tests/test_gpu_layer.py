@@ -309,3 +309,25 @@ def test_single_launch_routing_ties(dev, family, shape, groups):
         np.testing.assert_array_equal(from_dev(w_f), from_dev(w_m))
         np.testing.assert_array_equal(from_dev(of), from_dev(om))
     assert fused.sync_error() == 0
+
+
+@pytest.mark.parametrize("mode,gs", [("affine", 64), ("mxfp4", 32)])
+def test_layer_expert_major_gemv(dev, mode, gs):
+    """12 tokens over 16 experts (about 3 rows each): the kernel sequence runs
+    the expert-major GEMV; hidden 1536 gives 3 segment steps per gate/up row
+    and I 768 three per down row (several load-ring items per row)."""
+    import torch
+
+    from zmlx_amd.layer import QuantizedMoELayer
+
+    rng = np.random.default_rng(77)
+    H, E, I, K, B = 1536, 16, 768, 4, 12
+    banks, wr, sh, tq, tsh, wr_t = _build(dev, rng, H=H, E=E, I=I, K=K, mode=mode, gs=gs)
+    layer = QuantizedMoELayer.for_family("qwen3", wr_t, tq["gate"], tq["up"], tq["down"], top_k=K, group_size=gs,
+                                         mode=mode)
+    x = bf16_randn(rng, (B, H))
+    out, idx, w = layer(to_bf16(x, dev), return_routing=True)
+    torch.cuda.synchronize()
+    idx = from_dev(idx).astype(np.int64)
+    ref = _oracle_out(x, idx, O.bf16_round(from_dev(w)), banks, None, mode, gs, "native")
+    _cmp_out(from_dev(out), ref)

@@ -13,6 +13,9 @@
 #include "zmoe_grouped.h"
 #include "zmoe_host.h"
 
+#include <type_traits>
+#include <utility>
+
 namespace zmoe {
 
 constexpr int kQmvThreads = 256;
@@ -258,6 +261,51 @@ static int launch_qmv_l(hipStream_t st, int L, const void* x, const uint32_t* wg
 // rows' pair positions (scatter) or their sorted positions.
 // ---------------------------------------------------------------------------
 constexpr int kGemvRows = 128;  // weight rows per workgroup of the expert-major GEMV
+constexpr int kGqDepth = 4;     // items in the expert-major GEMV's load ring
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>), in order
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Quantisation parameters loaded raw and decoded at use (decoding right
+// after the load would make its wait immediate); decode_raw_q gives
+// load_param's values.
+struct RawQ {
+  uint32_t s, b;
+};
+template <int QMODE>
+__device__ __forceinline__ RawQ load_raw_q(const void* __restrict__ scales, const void* __restrict__ biases,
+                                           int64_t idx) {
+  RawQ r;
+  if (QMODE == ZMOE_Q_AFFINE) {
+    r.s = static_cast<const uint16_t*>(scales)[idx];
+    r.b = static_cast<const uint16_t*>(biases)[idx];
+  } else {
+    r.s = static_cast<const uint8_t*>(scales)[idx];
+    r.b = 0;
+  }
+  return r;
+}
+template <int QMODE>
+__device__ __forceinline__ SegParam decode_raw_q(RawQ r) {
+  SegParam p;
+  if (QMODE == ZMOE_Q_AFFINE) {
+    const float s = bf16_bits_to_f32(r.s);
+    const float b = bf16_bits_to_f32(r.b);
+    p.s = s;
+    p.c = b - 128.0f * s;
+  } else {
+    p.s = e8m0_to_f32(r.s);
+    p.c = 0.0f;
+  }
+  return p;
+}
 
 template <int L, int J, int NT, int QMODE, bool SWIGLU>
 __global__ __launch_bounds__(kQmvThreads) void k_grouped_qmv(GroupedArgs g, int gshift, int tiles) {
@@ -278,7 +326,6 @@ __global__ __launch_bounds__(kQmvThreads) void k_grouped_qmv(GroupedArgs g, int 
     stage_x_row<QMODE>(g.a + arow * g.lda, S, xs, sx, t);
   }
   __syncthreads();
-  constexpr int RPW = J * (kWave / L);
   const int wave = threadIdx.x / kWave;
   const int64_t wstride = static_cast<int64_t>(N) * (K >> 3);
   const int64_t pstride = static_cast<int64_t>(N) * ((QMODE == ZMOE_Q_AFFINE) ? (S >> gshift) : S);
@@ -289,39 +336,95 @@ __global__ __launch_bounds__(kQmvThreads) void k_grouped_qmv(GroupedArgs g, int 
                                             : nullptr;
   const uint32_t* wu = SWIGLU ? g.w1 + e * wstride : nullptr;
   const void* su = SWIGLU ? static_cast<const void*>(static_cast<const char*>(g.s1) + e * pstride * pbytes) : nullptr;
-  const void* bu = (SWIGLU && QMODE == ZMOE_Q_AFFINE)
+  const void* bu_ = (SWIGLU && QMODE == ZMOE_Q_AFFINE)
                        ? static_cast<const void*>(static_cast<const char*>(g.b1) + e * pstride * 2)
                        : nullptr;
-  // the block covers `tiles` consecutive row tiles (about kGemvRows rows) with
+  // The block covers `tiles` consecutive row tiles (about kGemvRows rows) with
   // one staging of the chunk's rows: the index loads and the staging are paid
-  // once for all of them
+  // once for all of them.  A wave's work is a flat list of items (row tile
+  // tt, segment step t), T = S / L steps per row; the loads of the next
+  // kGqDepth - 1 items are in flight while one is computed (loads are
+  // unconditional, the item index clamped at the end, so the wait counts
+  // stay exact).  Per row the arithmetic is wave_qmv's: segment steps
+  // accumulated in order, then the L-lane sum.
+  static_assert(J == 1, "one row group per wave and tile");
+  constexpr int RPW = kWave / L;
+  constexpr int D = kGqDepth;
   const int lane = threadIdx.x & (kWave - 1);
+  const int rs = lane / L, li = lane % L;
+  const int T = S / L;
+  const int64_t wpr = K >> 3;
+  const int64_t ppr = (QMODE == ZMOE_Q_AFFINE) ? (S >> gshift) : S;
+  const AffineK ak = affine_k();
   int64_t orow[NT];
 #pragma unroll
   for (int tok = 0; tok < NT; ++tok)
     orow[tok] = tok < ntok ? (g.scatter ? static_cast<int64_t>(g.sorted[r_begin + tok]) : r_begin + tok) : 0;
-  for (int tt = 0; tt < tiles; ++tt) {
-    const int row0 = ((blockIdx.x * tiles + tt) * kQmvWaves + wave) * RPW;
-    if (row0 >= N) break;
-    float rg[J][NT], ru[J][NT];
-    wave_qmv<L, J, NT, QMODE, SWIGLU>(wg, sg, bg, wu, su, bu, N, K, gshift, row0, ntok, xs, sx, rg, ru);
-    if ((lane % L) == 0) {
-      const int rs = lane / L;
+  // tiles of this block that hold rows for this wave
+  const int tile0 = blockIdx.x * tiles;
+  int ntl = 0;
+  while (ntl < tiles && ((tile0 + ntl) * kQmvWaves + wave) * RPW < N) ++ntl;
+  const int nitems = ntl * T;
+  if (nitems == 0) return;
+  uint4 bw[D], bu[D];
+  RawQ pgr[D], pur[D];
+  auto load_item = [&](int i, auto qc) {
+    constexpr int q = decltype(qc)::value;
+    const int it = min(i, nitems - 1);
+    const int tt = it / T, t = it - tt * T;
+    const int r = ((tile0 + tt) * kQmvWaves + wave) * RPW + rs;
+    const int64_t row = r < N ? r : N - 1;
+    const int sg_ = t * L + li;
+    const int gi = (QMODE == ZMOE_Q_AFFINE) ? (sg_ >> gshift) : sg_;
+    bw[q] = *reinterpret_cast<const uint4*>(wg + row * wpr + sg_ * 4);
+    if (SWIGLU) bu[q] = *reinterpret_cast<const uint4*>(wu + row * wpr + sg_ * 4);
+    pgr[q] = load_raw_q<QMODE>(sg, bg, row * ppr + gi);
+    if (SWIGLU) pur[q] = load_raw_q<QMODE>(su, bu_, row * ppr + gi);
+  };
+  float rg[NT], ru[NT];
 #pragma unroll
-      for (int j = 0; j < J; ++j) {
-        const int r = row0 + j * (kWave / L) + rs;
-        if (r < N) {
+  for (int tok = 0; tok < NT; ++tok) rg[tok] = ru[tok] = 0.0f;
+  auto compute_item = [&](int i, auto qc) {
+    constexpr int q = decltype(qc)::value;
+    const int tt = i / T, t = i - tt * T;
+    const int sg_ = t * L + li;
+    const SegParam pg = decode_raw_q<QMODE>(pgr[q]);
+    SegParam pu{0.0f, 0.0f};
+    if (SWIGLU) pu = decode_raw_q<QMODE>(pur[q]);
 #pragma unroll
-          for (int tok = 0; tok < NT; ++tok) {
-            if (tok < ntok) {
-              const uint32_t v = SWIGLU ? swiglu_bf16(round_bf16(rg[j][tok]), round_bf16(ru[j][tok]))
-                                        : f32_to_bf16_bits(rg[j][tok]);
-              g.out[orow[tok] * g.ldo + r] = static_cast<uint16_t>(v);
-            }
-          }
-        }
+    for (int tok = 0; tok < NT; ++tok) {
+      if (tok < ntok) {
+        const uint4 x0 = *reinterpret_cast<const uint4*>(xs + ((tok * 4 + 0) * S + sg_) * 4);
+        const uint4 x1 = *reinterpret_cast<const uint4*>(xs + ((tok * 4 + 1) * S + sg_) * 4);
+        const uint4 x2 = *reinterpret_cast<const uint4*>(xs + ((tok * 4 + 2) * S + sg_) * 4);
+        const uint4 x3 = *reinterpret_cast<const uint4*>(xs + ((tok * 4 + 3) * S + sg_) * 4);
+        const float xsum = (QMODE == ZMOE_Q_AFFINE) ? sx[tok * S + sg_] : 0.0f;
+        rg[tok] = seg_accum<QMODE>(rg[tok], pg.s, pg.c, seg_dot<QMODE>(bw[q], x0, x1, x2, x3, ak), xsum);
+        if (SWIGLU) ru[tok] = seg_accum<QMODE>(ru[tok], pu.s, pu.c, seg_dot<QMODE>(bu[q], x0, x1, x2, x3, ak), xsum);
       }
     }
+    if (t == T - 1) {
+      const int r = ((tile0 + tt) * kQmvWaves + wave) * RPW + rs;
+#pragma unroll
+      for (int tok = 0; tok < NT; ++tok) {
+        const float vg = wave_sum_width<L>(rg[tok]);
+        const float vu = SWIGLU ? wave_sum_width<L>(ru[tok]) : 0.0f;
+        if (li == 0 && r < N && tok < ntok) {
+          const uint32_t v = SWIGLU ? swiglu_bf16(round_bf16(vg), round_bf16(vu)) : f32_to_bf16_bits(vg);
+          g.out[orow[tok] * g.ldo + r] = static_cast<uint16_t>(v);
+        }
+        rg[tok] = ru[tok] = 0.0f;
+      }
+    }
+  };
+  // ring slot q holds item i with i % D == q
+  static_for<D - 1>([&](auto q) { load_item(decltype(q)::value, q); });
+  for (int i = 0; i < nitems; i += D) {
+    static_for<D>([&](auto q) {
+      constexpr int Q = decltype(q)::value;
+      load_item(i + Q + D - 1, std::integral_constant<int, (Q + D - 1) % D>{});
+      if (i + Q < nitems) compute_item(i + Q, q);
+    });
   }
 }
 
