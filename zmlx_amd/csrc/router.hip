@@ -15,19 +15,54 @@ constexpr int kRouterMaxK = kMaxTopK;
 // ---------------------------------------------------------------------------
 constexpr int kLogitTok = 4;   // tokens per block
 constexpr int kLogitRows = 1;  // rows per wave (short dependent chains: one row of wave sums per wave)
-
+constexpr int kLogitXv = 4;  // 16-byte x loads per thread per staging batch
+// PRE: 512-element chunks of a row loaded together (4 at hidden <= 2048, else 8)
+template <int PRE>
 __global__ __launch_bounds__(256) void k_dense_logits(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                                       int B, int E, int H, int out_f32, void* __restrict__ out) {
   extern __shared__ __align__(16) uint32_t xsm[];  // kLogitTok * H bf16
   const int b0 = blockIdx.y * kLogitTok;
   const int nt = min(kLogitTok, B - b0);
   const int hw = H >> 1;  // dwords per row
-  for (int i = threadIdx.x; i < nt * hw; i += blockDim.x) {
-    xsm[i] = reinterpret_cast<const uint32_t*>(x + static_cast<int64_t>(b0) * H)[i];
-  }
-  __syncthreads();
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int e0 = (blockIdx.x * 4 + wave) * kLogitRows;
+  const int nch = (H + 511) / 512;  // chunks of 512 elements (8 per lane)
+  // The router rows are cold in HBM: every chunk of a batch is loaded before
+  // any is used (and the first batch before the x staging), so a wave waits
+  // for one HBM round trip per batch instead of one per chunk.  Addresses are
+  // clamped and the lanes past H zeroed after the load, so the loads carry no
+  // branch.
+  uint4 wv[PRE][kLogitRows];
+  auto load_batch = [&](int cb) {
+#pragma unroll
+    for (int j = 0; j < PRE; ++j) {
+      const int h = (cb + j) * 512 + lane * 8;
+      const int hc = min(h, H - 8);
+#pragma unroll
+      for (int r = 0; r < kLogitRows; ++r) {
+        const int e = min(e0 + r, E - 1);
+        const uint4 v = *reinterpret_cast<const uint4*>(w + static_cast<int64_t>(e) * H + hc);
+        wv[j][r] = h < H ? v : make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  load_batch(0);
+  {
+    // x staged with 16-byte loads, a batch of kLogitXv per thread in flight
+    // before its LDS stores
+    const uint4* xg = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(b0) * H);
+    uint4* xs = reinterpret_cast<uint4*>(xsm);
+    const int nv = nt * (H >> 3);
+    for (int i0 = 0; i0 < nv; i0 += kLogitXv * 256) {
+      uint4 v[kLogitXv];
+#pragma unroll
+      for (int j = 0; j < kLogitXv; ++j) v[j] = xg[min(i0 + j * 256 + static_cast<int>(threadIdx.x), nv - 1)];
+#pragma unroll
+      for (int j = 0; j < kLogitXv; ++j)
+        if (i0 + j * 256 + static_cast<int>(threadIdx.x) < nv) xs[i0 + j * 256 + threadIdx.x] = v[j];
+    }
+  }
+  __syncthreads();
   if (e0 >= E) return;
   float acc[kLogitRows][kLogitTok];
 #pragma unroll
@@ -35,30 +70,29 @@ __global__ __launch_bounds__(256) void k_dense_logits(const uint16_t* __restrict
 #pragma unroll
     for (int t = 0; t < kLogitTok; ++t) acc[r][t] = 0.0f;
 
-  // chunks of 512 elements (8 per lane); each chunk's dot is reduced across
-  // the wave, then chunks are added in order -- the same order as the fused
-  // decode kernel, so both produce identical logits.
-  for (int c0 = 0; c0 < H; c0 += 512) {
-    const int h = c0 + lane * 8;
-    const bool valid = h < H;
-    uint4 wv[kLogitRows];
+  // each chunk's dot is reduced across the wave, then chunks are added in
+  // order -- the same order as the fused decode kernels, so both produce
+  // identical logits.
+  for (int cb = 0; cb < nch; cb += PRE) {
+    if (cb > 0) load_batch(cb);
 #pragma unroll
-    for (int r = 0; r < kLogitRows; ++r) {
-      const int e = min(e0 + r, E - 1);
-      wv[r] = valid ? *reinterpret_cast<const uint4*>(w + static_cast<int64_t>(e) * H + h) : make_uint4(0, 0, 0, 0);
-    }
+    for (int j = 0; j < PRE; ++j) {
+      if (cb + j >= nch) break;
+      const int h = (cb + j) * 512 + lane * 8;
+      const bool valid = h < H;
 #pragma unroll
-    for (int t = 0; t < kLogitTok; ++t) {
-      if (t < nt) {
-        const uint4 xv = valid ? *reinterpret_cast<const uint4*>(xsm + t * hw + (h >> 1)) : make_uint4(0, 0, 0, 0);
+      for (int t = 0; t < kLogitTok; ++t) {
+        if (t < nt) {
+          const uint4 xv = valid ? *reinterpret_cast<const uint4*>(xsm + t * hw + (h >> 1)) : make_uint4(0, 0, 0, 0);
 #pragma unroll
-        for (int r = 0; r < kLogitRows; ++r) {
-          float a = 0.0f;
-          a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv[r].x), __builtin_bit_cast(bf16x2_t, xv.x), a, false);
-          a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv[r].y), __builtin_bit_cast(bf16x2_t, xv.y), a, false);
-          a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv[r].z), __builtin_bit_cast(bf16x2_t, xv.z), a, false);
-          a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv[r].w), __builtin_bit_cast(bf16x2_t, xv.w), a, false);
-          acc[r][t] += wave_sum(a);
+          for (int r = 0; r < kLogitRows; ++r) {
+            float a = 0.0f;
+            a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv[j][r].x), __builtin_bit_cast(bf16x2_t, xv.x), a, false);
+            a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv[j][r].y), __builtin_bit_cast(bf16x2_t, xv.y), a, false);
+            a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv[j][r].z), __builtin_bit_cast(bf16x2_t, xv.z), a, false);
+            a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv[j][r].w), __builtin_bit_cast(bf16x2_t, xv.w), a, false);
+            acc[r][t] += wave_sum(a);
+          }
         }
       }
     }
@@ -175,7 +209,8 @@ extern "C" int zmoe_dense_logits(void* stream, const void* x, const void* w, int
   ZMOE_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0,
                ZMOE_EINVAL_SHAPE, "[dense_logits] x and w must be 16-byte aligned.");
   dim3 grid((E + 4 * kLogitRows - 1) / (4 * kLogitRows), (B + kLogitTok - 1) / kLogitTok);
-  hipLaunchKernelGGL(k_dense_logits, grid, dim3(256), static_cast<size_t>(kLogitTok) * H * 2, as_stream(stream),
+  hipLaunchKernelGGL(H <= 2048 ? k_dense_logits<4> : k_dense_logits<8>, grid, dim3(256),
+                     static_cast<size_t>(kLogitTok) * H * 2, as_stream(stream),
                      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), B, E, H,
                      out_dtype == ZMOE_DT_F32 ? 1 : 0, out);
   return check_launch("dense_logits");
