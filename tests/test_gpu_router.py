@@ -32,7 +32,7 @@ def test_dense_logits(dev):
     import zmlx_amd as Z
 
     rng = np.random.default_rng(0)
-    for B, E, H in [(1, 128, 2048), (5, 32, 2048), (3, 256, 7168), (16, 64, 2048), (6, 42, 1032), (2, 7, 4608)]:
+    for B, E, H in [(1, 128, 2048), (5, 32, 2048), (3, 256, 7168), (16, 64, 2048), (6, 42, 1032), (2, 7, 4608), (40, 64, 2048), (33, 20, 1032)]:
         x = bf16_randn(rng, (B, H))
         w = bf16_randn(rng, (E, H), 0.02)
         got = Z.dense_logits(to_bf16(x, dev), to_bf16(w, dev))

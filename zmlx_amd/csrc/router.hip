@@ -13,16 +13,19 @@ constexpr int kRouterMaxK = kMaxTopK;
 // ---------------------------------------------------------------------------
 // Dense router projection: logits[b, e] = x[b, :] . w[e, :]
 // ---------------------------------------------------------------------------
-constexpr int kLogitTok = 4;   // tokens per block
+// TOK tokens per block: 2 for decode batches up to 32 (more workgroups,
+// shorter wave-sum chains), 4 above (each token group re-reads the router
+// matrix, so larger batches take fewer groups)
+constexpr int kLogitTokMax = 4;
 constexpr int kLogitRows = 1;  // rows per wave (short dependent chains: one row of wave sums per wave)
 constexpr int kLogitXv = 4;  // 16-byte x loads per thread per staging batch
 // PRE: 512-element chunks of a row loaded together (4 at hidden <= 2048, else 8)
-template <int PRE>
+template <int TOK, int PRE>
 __global__ __launch_bounds__(256) void k_dense_logits(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                                       int B, int E, int H, int out_f32, void* __restrict__ out) {
-  extern __shared__ __align__(16) uint32_t xsm[];  // kLogitTok * H bf16
-  const int b0 = blockIdx.y * kLogitTok;
-  const int nt = min(kLogitTok, B - b0);
+  extern __shared__ __align__(16) uint32_t xsm[];  // TOK * H bf16
+  const int b0 = blockIdx.y * TOK;
+  const int nt = min(TOK, B - b0);
   const int hw = H >> 1;  // dwords per row
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int e0 = (blockIdx.x * 4 + wave) * kLogitRows;
@@ -64,11 +67,11 @@ __global__ __launch_bounds__(256) void k_dense_logits(const uint16_t* __restrict
   }
   __syncthreads();
   if (e0 >= E) return;
-  float acc[kLogitRows][kLogitTok];
+  float acc[kLogitRows][TOK];
 #pragma unroll
   for (int r = 0; r < kLogitRows; ++r)
 #pragma unroll
-    for (int t = 0; t < kLogitTok; ++t) acc[r][t] = 0.0f;
+    for (int t = 0; t < TOK; ++t) acc[r][t] = 0.0f;
 
   // each chunk's dot is reduced across the wave, then chunks are added in
   // order -- the same order as the fused decode kernels, so both produce
@@ -81,7 +84,7 @@ __global__ __launch_bounds__(256) void k_dense_logits(const uint16_t* __restrict
       const int h = (cb + j) * 512 + lane * 8;
       const bool valid = h < H;
 #pragma unroll
-      for (int t = 0; t < kLogitTok; ++t) {
+      for (int t = 0; t < TOK; ++t) {
         if (t < nt) {
           const uint4 xv = valid ? *reinterpret_cast<const uint4*>(xsm + t * hw + (h >> 1)) : make_uint4(0, 0, 0, 0);
 #pragma unroll
@@ -100,7 +103,7 @@ __global__ __launch_bounds__(256) void k_dense_logits(const uint16_t* __restrict
 #pragma unroll
   for (int r = 0; r < kLogitRows; ++r) {
 #pragma unroll
-    for (int t = 0; t < kLogitTok; ++t) {
+    for (int t = 0; t < TOK; ++t) {
       const float v = acc[r][t];
       if (lane == 0 && t < nt && e0 + r < E) {
         const int64_t o = static_cast<int64_t>(b0 + t) * E + e0 + r;
@@ -204,13 +207,15 @@ extern "C" int zmoe_dense_logits(void* stream, const void* x, const void* w, int
   ZMOE_REQUIRE(B >= 0 && E >= 1 && H >= 8 && H % 8 == 0, ZMOE_EINVAL_SHAPE, "[dense_logits] need H % 8 == 0.");
   ZMOE_REQUIRE(out_dtype == ZMOE_DT_BF16 || out_dtype == ZMOE_DT_F32, ZMOE_EINVAL_DTYPE,
                "[dense_logits] out dtype must be bf16 or f32.");
-  ZMOE_REQUIRE(static_cast<int64_t>(kLogitTok) * H * 2 <= 64 * 1024, ZMOE_EUNSUPPORTED, "[dense_logits] H too large.");
+  ZMOE_REQUIRE(static_cast<int64_t>(kLogitTokMax) * H * 2 <= 64 * 1024, ZMOE_EUNSUPPORTED, "[dense_logits] H too large.");
   if (B == 0) return ZMOE_OK;
   ZMOE_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0,
                ZMOE_EINVAL_SHAPE, "[dense_logits] x and w must be 16-byte aligned.");
-  dim3 grid((E + 4 * kLogitRows - 1) / (4 * kLogitRows), (B + kLogitTok - 1) / kLogitTok);
-  hipLaunchKernelGGL(H <= 2048 ? k_dense_logits<4> : k_dense_logits<8>, grid, dim3(256),
-                     static_cast<size_t>(kLogitTok) * H * 2, as_stream(stream),
+  const int tok = B <= 32 ? 2 : kLogitTokMax;
+  dim3 grid((E + 4 * kLogitRows - 1) / (4 * kLogitRows), (B + tok - 1) / tok);
+  auto fn = tok == 2 ? (H <= 2048 ? k_dense_logits<2, 4> : k_dense_logits<2, 8>)
+                     : (H <= 2048 ? k_dense_logits<kLogitTokMax, 4> : k_dense_logits<kLogitTokMax, 8>);
+  hipLaunchKernelGGL(fn, grid, dim3(256), static_cast<size_t>(tok) * H * 2, as_stream(stream),
                      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), B, E, H,
                      out_dtype == ZMOE_DT_F32 ? 1 : 0, out);
   return check_launch("dense_logits");
