@@ -1,0 +1,497 @@
+// XCD-partitioned one-token MoE decode layer (B = 1; the path of
+// zmoe_moe_layer for single-token decode, moe_mlp.py:787-1072 patched_call).
+//
+// MI355X has 8 XCDs of 32 CUs, each XCD with its own L2, and the dispatcher
+// deals the workgroups of a launch to the XCDs in turn.  A word that a CU
+// stores with an ordinary store stays in its XCD's L2, where device-scope
+// loads from the other CUs of the same XCD find it: an exchange inside one
+// XCD costs a fraction of one across the chip.  When the layer has exactly 8
+// units (top-8 routing and no shared expert, or top-7 plus one) this kernel
+// gives the 32 workgroups of XCD x unit x, so that the only exchanges that
+// leave an XCD are the 8 unit outputs of each output row:
+//
+//   R  every XCD computes all router logits: one wave per router row, the
+//      chunk sums of k_dense_logits, one tagged word (bf16 | tag << 16) per
+//      expert stored into the XCD's own region with an ordinary store;
+//   T  every wave polls the XCD's logits, computes the softmax and writes the
+//      routing keys to its own LDS copy; thread t ranks expert t / Q (as
+//      k_moe_decode1), and the expert of rank x becomes this XCD's unit;
+//   A  the XCD's 256 waves compute the unit's gate/up + SwiGLU rows (I / 256
+//      each) and store them, tagged, into the XCD's act row; each wave loads
+//      its down-projection items once its gate/up rows have arrived;
+//   D  every workgroup stages the act row from L2 (polling its tags) and
+//      computes its H / 32 output rows of the unit's down projection, stored
+//      as tagged words with device-scope stores;
+//   C  per 64-row chunk, the workgroup of the same index on XCD chunk % 8
+//      polls the 8 units' values and writes the k-ordered combine.
+//
+// The layer shape is a template constant (hidden 2048 on a 256-CU device,
+// expert intermediate I_), so the work assignment is folded at compile time.
+// Results are bit-identical to k_moe_decode1 and to the kernel sequence: the
+// same router chunk order, segment dots, wave sums and combine.
+#include "zmoe_decode1.h"
+
+#include <cstdlib>
+#include <type_traits>
+#include <vector>
+
+namespace zmoe {
+
+constexpr int kNX = 8;                        // XCDs
+constexpr int kXG = 256;                      // workgroups = CUs of MI355X
+constexpr int kXWX = kXG / kNX * kFWaves;     // waves per XCD
+constexpr int kXH = 2048;                     // hidden size
+
+__host__ __device__ constexpr int cgcd(int a, int b) { return b == 0 ? a : cgcd(b, a % b); }
+
+template <int I_>
+struct D1XShape {
+  static constexpr int H = kXH, S_H = kXH / 32, NC = kXH / 512;
+  static constexpr int S_I = I_ / 32;
+  static constexpr int RA = (I_ + kXWX - 1) / kXWX;   // gate/up rows per wave
+  static constexpr int RD = H / kXWX;                 // output rows per wave
+  static constexpr int LI = cgcd(S_I, kWave);         // lanes per down row
+  static constexpr int RPID = kWave / LI;             // down rows per load
+  static constexpr int TD = S_I / LI;                 // segments per lane and row
+  static constexpr int ND = ((RD + RPID - 1) / RPID) * TD;  // down items per wave
+  static_assert(I_ % 32 == 0 && H % kXWX == 0, "shape");
+  static_assert(RA <= kD1A && ND <= kD1D && RD * kNX <= kWave, "work per wave");
+};
+
+__device__ __forceinline__ int xcc_id() {
+  // HW_REG_XCC_ID (hardware register 20), bits [3:0]
+  return static_cast<int>(__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 0xF);
+}
+
+struct D1XLayout {
+  size_t xs, as, asx, yl, keys, total;
+};
+
+__host__ __device__ constexpr D1XLayout d1x_layout(int I) {
+  D1XLayout o{};
+  size_t off = (sizeof(D1Lds) + 15) & ~static_cast<size_t>(15);
+  o.xs = off;
+  off += static_cast<size_t>(lds_row_words(kXH / 32)) * 4;
+  o.as = off;
+  off += static_cast<size_t>(lds_row_words(I / 32)) * 4;
+  o.asx = off;
+  off += static_cast<size_t>(I / 32) * 4;
+  off = (off + 15) & ~static_cast<size_t>(15);
+  o.yl = off;
+  off += static_cast<size_t>(kFWaves) * kWave * 4;
+  o.keys = off;  // one copy of the routing keys per wave
+  off += static_cast<size_t>(kFWaves) * kD1RankMaxE * 4;
+  o.total = off;
+  return o;
+}
+
+template <int QMODE, int P, int I_>
+__global__ __launch_bounds__(kFThreads) void k_moe_decode1x(FusedParams p) {
+  using S = D1XShape<I_>;
+  constexpr D1XLayout lay = d1x_layout(I_);
+  extern __shared__ __align__(16) unsigned char smem[];
+  D1Lds& L = *reinterpret_cast<D1Lds*>(smem);
+  uint32_t* xs = reinterpret_cast<uint32_t*>(smem + lay.xs);
+  uint32_t* as = reinterpret_cast<uint32_t*>(smem + lay.as);
+  float* asx = reinterpret_cast<float*>(smem + lay.asx);
+  float* yl = reinterpret_cast<float*>(smem + lay.yl);
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int lane = __lane_id();
+  // the workgroups on physical XCD `xcd` (g, g + 8, g + 16, ...) compute unit
+  // `xcd`; gi is the index among them
+  const int xcd = xcc_id();
+  const int gi = blockIdx.x / kNX;
+  const int q = gi * kFWaves + wave;  // wave index within the XCD
+  const int E = p.E, K = p.K;
+  const AffineK ak = affine_k();
+
+  // phase stamps of thread 0, kept in registers and stored at the end
+  unsigned long long tsr[kTraceSlots];
+#pragma unroll
+  for (int i = 0; i < kTraceSlots; ++i) tsr[i] = 0;
+  auto mark = [&](int i) {
+    if (p.trace) tsr[i] = wall_clock64();
+  };
+  mark(0);
+  const unsigned epoch = dev_load(p.sync + kEpochWord + blockIdx.x);
+  const unsigned tag16 = (epoch + 1u) & 0xFFFFu;
+
+  // ---------------- R: router logits, XCD-local ----------------
+  uint32_t* lg = reinterpret_cast<uint32_t*>(p.rpart) + E * (1 + xcd);
+  {
+    // x in registers: lane l holds elements 8 l .. 8 l + 7 of each 512-chunk
+    uint4 xv[S::NC];
+#pragma unroll
+    for (int c = 0; c < S::NC; ++c) xv[c] = gload(reinterpret_cast<const uint4*>(p.x + c * 512 + lane * 8));
+    for (int u = q; u < E; u += kXWX) {
+      uint4 wv[S::NC];
+#pragma unroll
+      for (int c = 0; c < S::NC; ++c)
+        wv[c] = gload(reinterpret_cast<const uint4*>(p.wr + static_cast<int64_t>(u) * kXH + c * 512 + lane * 8));
+      float a = 0.0f;
+#pragma unroll
+      for (int c = 0; c < S::NC; ++c) {
+        float d = 0.0f;
+        d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv[c].x), __builtin_bit_cast(bf16x2_t, xv[c].x), d, false);
+        d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv[c].y), __builtin_bit_cast(bf16x2_t, xv[c].y), d, false);
+        d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv[c].z), __builtin_bit_cast(bf16x2_t, xv[c].z), d, false);
+        d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv[c].w), __builtin_bit_cast(bf16x2_t, xv[c].w), d, false);
+        a += wave_sum(d);  // chunks in order
+      }
+      // an ordinary store: the word stays in this XCD's L2 for its readers
+      if (lane == 0) gstore(lg + u, (tag16 << 16) | f32_to_bf16_bits(a));
+    }
+    // wave 0 writes the x tile in stage_rows_lds's layout: item (segment
+    // c * 16 + l / 4, quarter l % 4); each lane forms its segment's sum in A
+    if (wave == 0) {
+#pragma unroll
+      for (int c = 0; c < S::NC; ++c) {
+        const uint4 v = xv[c];
+        uint4 o = v;
+        if (QMODE == ZMOE_Q_AFFINE) {
+          o.x = (v.x & 0xFFFFu) | (v.z << 16);
+          o.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
+          o.z = (v.y & 0xFFFFu) | (v.w << 16);
+          o.w = (v.y >> 16) | (v.w & 0xFFFF0000u);
+        }
+        *reinterpret_cast<uint4*>(xs + ((lane & 3) * S::S_H + c * 16 + (lane >> 2)) * 4) = o;
+      }
+    }
+  }
+  mark(1);
+
+  // ---------------- T: routing ----------------
+  // Every wave polls the logits, computes the softmax and writes the unique
+  // keys (bf16 value order, then lower index first) to its own LDS copy;
+  // thread t ranks expert t / Q against its wave's copy, so no workgroup
+  // barrier sits between the logits and the ranks.
+  const int Epad = E <= 64 ? 64 : (E <= 128 ? 128 : 256);
+  uint32_t* keys = reinterpret_cast<uint32_t*>(smem + lay.keys) + wave * Epad;
+  {
+    RowVals<P> row;
+    for (unsigned n = 0;; ++n) {
+      uint32_t wd[P];
+#pragma unroll
+      for (int i = 0; i < P; ++i) wd[i] = dev_load(lg + min(lane + 64 * i, E - 1));
+      bool ok = true;
+#pragma unroll
+      for (int i = 0; i < P; ++i) {
+        ok = ok && (wd[i] >> 16) == tag16;
+        row.v[i] = lane + 64 * i < E ? bf16_bits_to_f32(wd[i] & 0xFFFFu) : -INFINITY;
+      }
+      if (__all(ok)) break;
+      if (n > kSpinLimit) {
+        if (lane == 0) wait_timeout(p);
+        break;
+      }
+    }
+    mark(3);
+    float(&v)[P] = row.v;
+    if (p.route.kind == kRouteSoftmaxProbs) {
+      // moe_mlp.py:255-266: precise softmax, probabilities rounded to bf16
+      const float m = reg_row_max(v, E);
+#pragma unroll
+      for (int i = 0; i < P; ++i) v[i] = expf(v[i] - m);
+      const float sum = reg_row_sum(v, E);
+#pragma unroll
+      for (int i = 0; i < P; ++i) v[i] = div_to_bf16(v[i], sum);
+    }
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+      const int e = lane + 64 * i;
+      if (e < Epad) keys[e] = e < E ? ((order_key(v[i]) & 0xFFFF0000u) | (0xFFFFu - static_cast<uint32_t>(e))) : 0u;
+    }
+  }
+  wave_lds_sync();
+  {
+    int i, r;
+    uint32_t ki;
+    if (Epad == 64) r = rank_in_row<64>(keys, i, ki);
+    else if (Epad == 128) r = rank_in_row<128>(keys, i, ki);
+    else r = rank_in_row<256>(keys, i, ki);
+    if (r >= 0 && i < E && r < K) {
+      const uint32_t ok = ki >> 16;
+      const uint32_t u16 = (ok & 0x8000u) ? (ok & 0x7FFFu) : (~ok & 0xFFFFu);
+      L.route.sel[r] = i;
+      L.route.sval[r] = __uint_as_float(u16 << 16);
+      if (r == xcd) {
+#pragma unroll
+        for (int m = 0; m < 3; ++m) set_unit_e(p, L, 0, m, i);
+      }
+    }
+    if (K == xcd && threadIdx.x == kFThreads - 1) {  // the shared expert's XCD
+#pragma unroll
+      for (int m = 0; m < 3; ++m) set_unit_e(p, L, 0, m, -1);
+    }
+  }
+  mark(4);
+  lds_barrier();
+  mark(5);
+
+  // ---------------- A: gate/up + SwiGLU of unit xcd ----------------
+  // The gate/up rows are loaded first and alone; each wave loads its
+  // down-projection items once its gate/up rows have arrived, so the act
+  // rows are not queued behind down-projection bytes.
+  constexpr int64_t wpr = kXH / 8;
+  const int ppr = (QMODE == ZMOE_Q_AFFINE) ? (S::S_H >> p.gshift) : S::S_H;
+  const int pi = (QMODE == ZMOE_Q_AFFINE) ? (lane >> p.gshift) : lane;
+  const int a_r0 = q * S::RA;  // gate/up rows [a_r0, a_r0 + RA)
+  uint4 wg[S::RA], wu[S::RA];
+  RawParam rg[S::RA], ru[S::RA];
+  {
+    const uint32_t* gw = L.w[0][0] + lane * 4;
+    const uint32_t* uw = L.w[1][0] + lane * 4;
+    const void *gs = L.s[0][0], *gb = L.b[0][0], *us = L.s[1][0], *ub = L.b[1][0];
+#pragma unroll
+    for (int j = 0; j < S::RA; ++j) {
+      const int r = min(a_r0 + j, I_ - 1);  // past the last row: repeat it
+      wg[j] = gload(reinterpret_cast<const uint4*>(gw + r * wpr));
+      wu[j] = gload(reinterpret_cast<const uint4*>(uw + r * wpr));
+      rg[j] = seg_param_load<QMODE>(gs, gb, r * ppr + pi);
+      ru[j] = seg_param_load<QMODE>(us, ub, r * ppr + pi);
+    }
+  }
+  mark(13);
+  if (wave == 0) rank_weights(p, L, K);
+  uint32_t actw;
+  {
+    const uint4 x0 = *reinterpret_cast<const uint4*>(xs + ((0 * S::S_H) + lane) * 4);
+    const uint4 x1 = *reinterpret_cast<const uint4*>(xs + ((1 * S::S_H) + lane) * 4);
+    const uint4 x2 = *reinterpret_cast<const uint4*>(xs + ((2 * S::S_H) + lane) * 4);
+    const uint4 x3 = *reinterpret_cast<const uint4*>(xs + ((3 * S::S_H) + lane) * 4);
+    // sum of the lane's x segment, in stage_rows_lds's order
+    float xsum = 0.0f;
+    if (QMODE == ZMOE_Q_AFFINE) {
+      const uint4 xq[4] = {x0, x1, x2, x3};
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint4 o = xq[w];
+        xsum += bf16_bits_to_f32(o.x & 0xFFFFu) + bf16_bits_to_f32(o.y & 0xFFFFu);
+        xsum += bf16_bits_to_f32(o.z & 0xFFFFu) + bf16_bits_to_f32(o.w & 0xFFFFu);
+        xsum += bf16_bits_to_f32(o.x >> 16) + bf16_bits_to_f32(o.y >> 16);
+        xsum += bf16_bits_to_f32(o.z >> 16) + bf16_bits_to_f32(o.w >> 16);
+      }
+    }
+    float gsel = 0.0f, usel = 0.0f;
+#pragma unroll
+    for (int j = 0; j < S::RA; ++j) {
+      float sg, cg, su, cu2;
+      seg_param_decode<QMODE>(rg[j], sg, cg);
+      seg_param_decode<QMODE>(ru[j], su, cu2);
+      const float gv = wave_sum(seg_accum<QMODE>(0.0f, sg, cg, seg_dot<QMODE>(wg[j], x0, x1, x2, x3, ak), xsum));
+      const float uv = wave_sum(seg_accum<QMODE>(0.0f, su, cu2, seg_dot<QMODE>(wu[j], x0, x1, x2, x3, ak), xsum));
+      if (lane == j) {
+        gsel = gv;
+        usel = uv;
+      }
+    }
+    actw = (tag16 << 16) | swiglu_bf16(round_bf16(gsel), round_bf16(usel));
+  }
+  mark(6);
+  // down-projection items: lane group rs (of RPID) takes row h0 + g * RPID +
+  // rs, lane li of it segments t * LI + li
+  const int h0 = q * S::RD;
+  const int rsD = lane / S::LI, liD = lane % S::LI;
+  constexpr int64_t wprD = I_ / 8;
+  const int pprD = (QMODE == ZMOE_Q_AFFINE) ? (S::S_I >> p.gshift) : S::S_I;
+  uint4 wd[S::ND];
+  RawParam rd[S::ND];
+  {
+    const uint32_t* dw = L.w[2][0];
+    const void *ds = L.s[2][0], *db = L.b[2][0];
+#pragma unroll
+    for (int j = 0; j < S::ND; ++j) {
+      const int g = j / S::TD, t = j % S::TD;
+      const int row = h0 + min(g * S::RPID + rsD, S::RD - 1);
+      const int s = t * S::LI + liD;
+      wd[j] = gload(reinterpret_cast<const uint4*>(dw + row * wprD + s * 4));
+      rd[j] = seg_param_load<QMODE>(ds, db, row * pprD + ((QMODE == ZMOE_Q_AFFINE) ? (s >> p.gshift) : s));
+    }
+  }
+  if (lane < S::RA && a_r0 + lane < I_) gstore(p.act + static_cast<int64_t>(xcd) * p.act_stride + a_r0 + lane, actw);
+  mark(7);
+
+  // ---------------- D: the unit's act row from L2, down projection ----------------
+  stage_rows_lds<QMODE, true>(p, p.act + static_cast<int64_t>(xcd) * p.act_stride, p.act_stride, 1, S::S_I, as, asx,
+                              tag16, p.by_S4I, p.by_SI);
+  mark(8);
+  lds_barrier();
+  mark(9);
+  float ysum[S::ND];
+  {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < S::ND; ++j) {
+      const int t = j % S::TD;
+      const int s = t * S::LI + liD;
+      float sdj, cdj;
+      seg_param_decode<QMODE>(rd[j], sdj, cdj);
+      const float xsum = (QMODE == ZMOE_Q_AFFINE) ? asx[s] : 0.0f;
+      acc = seg_accum<QMODE>(t == 0 ? 0.0f : acc, sdj, cdj, seg_dot_lds<QMODE>(wd[j], as, S::S_I, 0, s, ak), xsum);
+      ysum[j] = (t == S::TD - 1) ? wave_sum_width<S::LI>(acc) : 0.0f;
+    }
+  }
+  mark(11);
+#pragma unroll
+  for (int j = 0; j < S::ND; ++j) {
+    const int g = j / S::TD, t = j % S::TD;
+    const int hl = g * S::RPID + rsD;
+    if (t == S::TD - 1 && liD == 0 && hl < S::RD)
+      dev_store(p.xy + static_cast<int64_t>(xcd) * kXH + h0 + hl, (tag16 << 16) | f32_to_bf16_bits(ysum[j]));
+  }
+  mark(10);
+
+  // ---------------- C: k-ordered combine of the chunk, on one XCD ----------------
+  // chunk = the 8 * RD output rows of the workgroups with index gi; each
+  // wave of the combining workgroup takes its own RD rows: lane k * RD + r
+  // polls unit k's value of row h0 + r.
+  if (xcd == gi % kNX) {
+    const int k = lane / S::RD, r = lane % S::RD;
+    const bool mine = k < kNX;
+    const uint32_t* src = p.xy + static_cast<int64_t>(mine ? k : 0) * kXH + h0 + r;
+    uint32_t v = 0;
+    for (unsigned spins = 0;; ++spins) {
+      v = dev_load(src);
+      if (__all(!mine || (v >> 16) == tag16)) break;
+      if (spins > kSpinLimit) {
+        if (lane == 0) wait_timeout(p);
+        break;
+      }
+    }
+    float* yw = yl + wave * kWave;
+    if (mine) yw[r * kNX + k] = bf16_bits_to_f32(v & 0xFFFFu);
+    wave_lds_sync();
+    if (lane < S::RD) {
+      const float* yr = yw + lane * kNX;
+      const float* wk = L.route.w;
+      float o = round_bf16(combine_one(p.combine_mode, K, [&](int kk) { return yr[kk]; }, [&](int kk) { return wk[kk]; }));
+      if (K < kNX) o = add_nofma(o, yr[K]);
+      gstore(p.out + h0 + lane, static_cast<uint16_t>(f32_to_bf16_bits(o)));
+    }
+  }
+  mark(12);
+  if (threadIdx.x == 0) {
+    dev_store(p.sync + kEpochWord + blockIdx.x, epoch + 1);
+    if (p.trace) {
+#pragma unroll
+      for (int i = 0; i < kTraceSlots; ++i)
+        if (tsr[i]) gstore(p.trace + blockIdx.x * kTraceSlots + i, tsr[i]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+static bool d1x_enabled() {
+  static int on = -1;
+  if (on < 0) {
+    const char* e = getenv("ZMOE_DECODE1X");
+    on = (e && e[0] == '0') ? 0 : 1;
+  }
+  return on == 1;
+}
+
+// Intermediate sizes with a compiled kernel (Qwen3-30B-A3B: 768; OLMoE: 1024).
+static bool d1x_inter_ok(int I) { return I == 768 || I == 1024; }
+
+size_t xcd_rpart_bytes(const zmoe_layer_desc* d) { return static_cast<size_t>(kNX + 1) * d->n_experts * 4; }
+size_t xcd_xy_bytes(const zmoe_layer_desc* d) { return static_cast<size_t>(kNX) * d->hidden * 4; }
+
+__global__ void k_xcc_probe(unsigned* out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = static_cast<unsigned>(xcc_id());
+}
+
+// Whether the workgroups of a G-workgroup launch are dealt to the 8 XCDs in
+// turn (workgroup g on XCD (s + g) % 8 for some s) on the current device:
+// probed once per device with a small kernel whose result is copied back
+// (scratch: G words of device memory).  While a stream is being captured
+// nothing can be copied back, so an unprobed device counts as "no" (the layer
+// then runs k_moe_decode1) until a call outside capture.
+static int g_xcd_rr[64];
+
+static bool xcd_round_robin(hipStream_t st, unsigned* scratch, int G) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  if (g_xcd_rr[dev]) return g_xcd_rr[dev] == 1;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
+  hipLaunchKernelGGL(k_xcc_probe, dim3(G), dim3(kFThreads), 0, st, scratch);
+  std::vector<unsigned> h(G, ~0u);
+  if (hipGetLastError() != hipSuccess ||
+      hipMemcpyAsync(h.data(), scratch, static_cast<size_t>(G) * 4, hipMemcpyDeviceToHost, st) != hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess) {
+    g_xcd_rr[dev] = 2;
+    return false;
+  }
+  bool ok = true;
+  for (int g = 0; g < G; ++g) ok = ok && h[g] == (h[0] + static_cast<unsigned>(g)) % kNX;
+  g_xcd_rr[dev] = ok ? 1 : 2;
+  return ok;
+}
+
+static size_t d1x_lds_bytes(int I) {
+  const size_t need = d1x_layout(I).total;
+  // at least 96 KiB: one workgroup per CU, so the 32 workgroups of an XCD
+  // sit on its 32 CUs
+  return need > 96 * 1024 ? need : 96 * 1024;
+}
+
+static bool d1x_shape_ok(const zmoe_layer_desc* d, int G) {
+  if (!d1x_enabled() || G != kXG) return false;
+  const int Uall = d->top_k + (d->shared_inter > 0 ? 1 : 0);
+  if (Uall != kNX || d->top_k > kMaxTopK) return false;
+  if (d->shared_inter > 0 && d->shared_inter != d->inter) return false;
+  if (d->hidden != kXH || !d1x_inter_ok(d->inter)) return false;
+  const bool rank_route = d->router_kind == ZMOE_ROUTER_SOFTMAX_PROBS ||
+                          (d->router_kind == ZMOE_ROUTER_TOPK_LOGITS && d->router_bias == nullptr && d->norm_topk_prob);
+  if (!rank_route || d->n_experts > kD1RankMaxE || d->n_experts > kXWX) return false;
+  return d1x_lds_bytes(d->inter) <= 160 * 1024;
+}
+
+template <int QMODE, int P, int I_>
+static int launch_d1x_t(hipStream_t st, const FusedParams& fp) {
+  static bool prepared = false;
+  const void* fn = reinterpret_cast<const void*>(&k_moe_decode1x<QMODE, P, I_>);
+  const size_t lds = d1x_lds_bytes(I_);
+  if (!prepared) {
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    prepared = true;
+  }
+  int occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, kFThreads, lds) != hipSuccess || occ < 1)
+    return fail(ZMOE_EUNSUPPORTED, "[moe_layer] XCD-partitioned kernel cannot be resident on every CU");
+  hipLaunchKernelGGL((k_moe_decode1x<QMODE, P, I_>), dim3(kXG), dim3(kFThreads), lds, st, fp);
+  return check_launch("moe_layer(XCD-partitioned one-token launch)");
+}
+
+template <int QMODE, int I_>
+static int launch_d1x_p(hipStream_t st, const FusedParams& fp) {
+  switch (route_slots(fp.E)) {
+    case 1: return launch_d1x_t<QMODE, 1, I_>(st, fp);
+    case 2: return launch_d1x_t<QMODE, 2, I_>(st, fp);
+    default: return launch_d1x_t<QMODE, 4, I_>(st, fp);
+  }
+}
+
+template <int QMODE>
+static int launch_d1x_q(hipStream_t st, const FusedParams& fp) {
+  return fp.I == 768 ? launch_d1x_p<QMODE, 768>(st, fp) : launch_d1x_p<QMODE, 1024>(st, fp);
+}
+
+int try_decode1x(hipStream_t st, const zmoe_layer_desc* d, const FusedParams& fp_in, int grid) {
+  if (!d1x_shape_ok(d, grid) || fp_in.xy == nullptr) return -1;
+  if (!xcd_round_robin(st, fp_in.xy, grid)) return -1;
+  FusedParams fp = fp_in;
+  for (int m = 0; m < 3; ++m) {
+    const int64_t N = (m == 2) ? d->hidden : d->inter, Kin = (m == 2) ? d->inter : d->hidden;
+    const int64_t groups = (d->quant_mode == ZMOE_Q_AFFINE) ? Kin / d->group_size : Kin / 32;
+    fp.d1.wst[m] = N * (Kin / 8);
+    fp.d1.sst[m] = N * groups * ((d->quant_mode == ZMOE_Q_AFFINE) ? 2 : 1);
+  }
+  if (d->quant_mode == ZMOE_Q_AFFINE) return launch_d1x_q<ZMOE_Q_AFFINE>(st, fp);
+  return launch_d1x_q<ZMOE_Q_MXFP4>(st, fp);
+}
+
+}  // namespace zmoe

@@ -519,7 +519,9 @@ bool fused_supported(const zmoe_layer_desc* d, int B) {
 // workspace: state block | rpart | act | trace
 static size_t off_rpart() { return kSyncBlockBytes; }
 static size_t off_act(const zmoe_layer_desc* d, int B) {
-  return align256(off_rpart() + static_cast<size_t>(B) * d->n_experts * (d->hidden / 512) * 8);
+  size_t rpart = static_cast<size_t>(B) * d->n_experts * (d->hidden / 512) * 8;
+  if (B == 1 && xcd_rpart_bytes(d) > rpart) rpart = xcd_rpart_bytes(d);  // one XCD-local copy per XCD
+  return align256(off_rpart() + rpart);
 }
 static size_t off_flags(const zmoe_layer_desc* d, int B) {
   const int stride = d->inter > d->shared_inter ? d->inter : d->shared_inter;
@@ -530,8 +532,12 @@ static size_t off_trace(const zmoe_layer_desc* d, int B) {
   return align256(off_flags(d, B) + 4096 + static_cast<size_t>(num_cus()) * 4);
 }
 
+static size_t off_xy(const zmoe_layer_desc* d, int B) {
+  return align256(off_trace(d, B) + static_cast<size_t>(num_cus()) * kTraceSlots * 8);
+}
+
 size_t fused_workspace_bytes(const zmoe_layer_desc* d, int B) {
-  return off_trace(d, B) + static_cast<size_t>(num_cus()) * kTraceSlots * 8;
+  return off_xy(d, B) + (B == 1 ? xcd_xy_bytes(d) : 0);
 }
 
 size_t fused_trace_info(const zmoe_layer_desc* d, int B, int* n_blocks, int* n_slots) {
@@ -612,6 +618,7 @@ int launch_fused(hipStream_t st, const zmoe_layer_desc* d, const void* x, int B,
   fp.out_idx = out_idx;
   fp.out_w = out_w;
   fp.trace = (d->flags & ZMOE_LAYER_TRACE) ? reinterpret_cast<unsigned long long*>(base + off_trace(d, B)) : nullptr;
+  fp.xy = B == 1 ? reinterpret_cast<uint32_t*>(base + off_xy(d, B)) : nullptr;
   fp.by_S4H = make_fastdiv(static_cast<uint32_t>(d->hidden / 8));
   fp.by_SH = make_fastdiv(static_cast<uint32_t>(d->hidden / 32));
   fp.by_S4I = make_fastdiv(static_cast<uint32_t>(d->inter / 8));

@@ -58,6 +58,7 @@ struct FusedParams {
   uint32_t* out_idx;
   float* out_w;
   unsigned long long* trace;  // nullable: [G][kTraceSlots] realtime stamps
+  uint32_t* xy;          // XCD-partitioned one-token kernel: [8][H] tagged expert outputs (bf16 | tag << 16)
   FastDiv by_S4H, by_SH, by_S4I, by_SI;  // staged-row items: S*4 and S per row
   D1Plan d1;
 };
@@ -84,7 +85,7 @@ __device__ __forceinline__ void wait_timeout(const FusedParams& p) {
 // carries `tag`, rounded to bf16 (the gate Linear returns bf16 logits).
 template <int P>
 __device__ __forceinline__ RowVals<P> poll_logits(const FusedParams& p, const unsigned long long* rp, int NC,
-                                                  unsigned tag) {
+                                                  unsigned tag, int backoff = 0) {
   const int lane = __lane_id();
   RowVals<P> row;
   unsigned n = 0;
@@ -116,6 +117,7 @@ __device__ __forceinline__ RowVals<P> poll_logits(const FusedParams& p, const un
       if (lane == 0) wait_timeout(p);
       break;
     }
+    if (backoff) __builtin_amdgcn_s_sleep(1);
   }
   return row;
 }
@@ -141,7 +143,7 @@ __host__ __device__ constexpr int lds_row_words(int S) { return 16 * S + 32; }
 template <int QMODE, bool DEV, int NI = 2>
 __device__ __forceinline__ void stage_rows_lds(const FusedParams& p, const void* __restrict__ src, int64_t src_stride,
                                                int nrows, int S, uint32_t* xs, float* sx, unsigned tag16,
-                                               FastDiv by_S4, FastDiv by_S) {
+                                               FastDiv by_S4, FastDiv by_S, int backoff = 0) {
   // (row, segment, quarter) items, NI per thread per round, all of a round's
   // loads in flight together
   const int S4 = S * 4;
@@ -178,6 +180,7 @@ __device__ __forceinline__ void stage_rows_lds(const FusedParams& p, const void*
           wait_timeout(p);
           break;
         }
+        if (backoff) __builtin_amdgcn_s_sleep(1);
 #pragma unroll
         for (int h = 0; h < NI; ++h) {
           unsigned long long d[4];
@@ -286,6 +289,14 @@ __device__ __forceinline__ void seg_param_decode(RawParam r, float& s, float& c)
 // One-token kernel (decode1.hip): used by launch_fused for B = 1 when it
 // supports the shape (ZMOE_DECODE1=0 in the environment turns it off).
 bool decode1_supported(const zmoe_layer_desc* d, int grid);
+// XCD-partitioned one-token kernel (decode1.hip): tried first by
+// launch_decode1 (ZMOE_DECODE1X=0 turns it off).  Workspace beyond the
+// one-token kernel's: the router partials of each XCD (xcd_rpart_bytes at
+// fp.rpart) and the tagged expert outputs (xcd_xy_bytes at fp.xy).
+size_t xcd_rpart_bytes(const zmoe_layer_desc* d);
+size_t xcd_xy_bytes(const zmoe_layer_desc* d);
+// Launches it when it applies (returns its status), else returns -1.
+int try_decode1x(hipStream_t st, const zmoe_layer_desc* d, const FusedParams& fp, int grid);
 int launch_decode1(hipStream_t st, const zmoe_layer_desc* d, const FusedParams& fp, int grid);
 // Batched kernel (decodeb.hip): 2 <= B <= 16 at hidden 2048
 // (ZMOE_DECODEB=0 turns it off).
