@@ -63,6 +63,51 @@ __device__ __forceinline__ int xcc_id() {
   return static_cast<int>(__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 0xF);
 }
 
+// Loads for words that other CUs of this XCD stored with ordinary stores
+// (XCD-local exchange): the sc0 nt cache policy skips the CU's L1 and is
+// served by the XCD's L2, where those stores land.  (Loads that do not skip
+// L1 can keep returning a stale line; device-scope loads also see the words
+// but take about twice as long under streaming load.)  The compiler's wait
+// counts do not cover these loads, so each waits for its own results, and
+// with them for every load the wave issued before.
+template <int P>
+__device__ __forceinline__ void xcd_load_row(const uint32_t* lg, int E, uint32_t (&wd)[P]) {
+  const int lane = __lane_id();
+  const uint32_t* a0 = lg + min(lane, E - 1);
+  if constexpr (P == 1) {
+    asm volatile("global_load_dword %0, %1, off sc0 nt\n\ts_waitcnt vmcnt(0)" : "=v"(wd[0]) : "v"(a0) : "memory");
+  } else if constexpr (P == 2) {
+    const uint32_t* a1 = lg + min(lane + 64, E - 1);
+    asm volatile("global_load_dword %0, %2, off sc0 nt\n\tglobal_load_dword %1, %3, off sc0 nt\n\ts_waitcnt vmcnt(0)"
+                 : "=&v"(wd[0]), "=&v"(wd[1])
+                 : "v"(a0), "v"(a1)
+                 : "memory");
+  } else {
+    static_assert(P == 4, "route slots");
+    const uint32_t* a1 = lg + min(lane + 64, E - 1);
+    const uint32_t* a2 = lg + min(lane + 128, E - 1);
+    const uint32_t* a3 = lg + min(lane + 192, E - 1);
+    asm volatile(
+        "global_load_dword %0, %4, off sc0 nt\n\tglobal_load_dword %1, %5, off sc0 nt\n\t"
+        "global_load_dword %2, %6, off sc0 nt\n\tglobal_load_dword %3, %7, off sc0 nt\n\ts_waitcnt vmcnt(0)"
+        : "=&v"(wd[0]), "=&v"(wd[1]), "=&v"(wd[2]), "=&v"(wd[3])
+        : "v"(a0), "v"(a1), "v"(a2), "v"(a3)
+        : "memory");
+  }
+}
+__device__ __forceinline__ void xcd_load_2x128(const uint32_t* ptr, uint4& a, uint4& b) {
+  asm volatile("global_load_dwordx4 %0, %2, off sc0 nt\n\tglobal_load_dwordx4 %1, %2, off offset:16 sc0 nt\n\ts_waitcnt vmcnt(0)"
+               : "=&v"(a), "=&v"(b)
+               : "v"(ptr)
+               : "memory");
+}
+
+// Spin limit of this kernel's waits (each poll is an L2 or memory round
+// trip; a wait that is satisfied takes a few microseconds).  After one wait
+// of a wave gives up, its later waits give up at once, so a launch whose
+// exchanges fail still ends within milliseconds.
+constexpr unsigned kXSpinLimit = 1u << 16;
+
 struct D1XLayout {
   size_t xs, as, asx, yl, keys, total;
 };
@@ -85,8 +130,35 @@ __host__ __device__ constexpr D1XLayout d1x_layout(int I) {
   return o;
 }
 
+// Kernel arguments: everything the kernel reads from its argument block,
+// loaded into scalar registers in one batch at the start (an argument read
+// first on the critical path costs a scalar-cache miss there).
+struct D1XArgs {
+  const uint16_t* x;
+  uint16_t* out;
+  const uint16_t* wr;
+  const uint32_t* w[4];   // gate, up, down, and the shared expert's gate (its up/down follow in sh)
+  const void* s[3];
+  const void* b[3];
+  const uint32_t* shw[3];  // shared expert (unit K when top-7 + shared)
+  const void* shs[3];
+  const void* shb[3];
+  int64_t wst[3], sst[3];  // per-expert strides: packed words, scale (= bias) bytes
+  unsigned* sync;
+  uint32_t* lg;            // [1 + 8][E] logit words (region 1 + x: XCD x)
+  uint32_t* act;           // [8][act_stride] act words, row x: XCD x
+  uint32_t* xy;            // [8][H] unit outputs
+  uint32_t* out_idx;
+  float* out_w;
+  unsigned long long* trace;
+  int E, K, gshift, combine_mode, act_stride;
+  int route_kind, norm, w_bf16;
+};
+
+#define ZMOE_PIN(v) asm volatile("" : "+s"(v))
+
 template <int QMODE, int P, int I_>
-__global__ __launch_bounds__(kFThreads) void k_moe_decode1x(FusedParams p) {
+__global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
   using S = D1XShape<I_>;
   constexpr D1XLayout lay = d1x_layout(I_);
   extern __shared__ __align__(16) unsigned char smem[];
@@ -96,6 +168,36 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(FusedParams p) {
   float* asx = reinterpret_cast<float*>(smem + lay.asx);
   float* yl = reinterpret_cast<float*>(smem + lay.yl);
 
+  // every argument, in scalar registers before the first use
+  const uint16_t* x = a.x;
+  const uint16_t* wr = a.wr;
+  unsigned* sync = a.sync;
+  uint32_t* lg0 = a.lg;
+  int E = a.E, K = a.K, gshift = a.gshift;
+  ZMOE_PIN(x); ZMOE_PIN(wr); ZMOE_PIN(sync); ZMOE_PIN(lg0); ZMOE_PIN(E); ZMOE_PIN(K); ZMOE_PIN(gshift);
+  const uint32_t* mw[3] = {a.w[0], a.w[1], a.w[2]};
+  const void* ms[3] = {a.s[0], a.s[1], a.s[2]};
+  const void* mb[3] = {a.b[0], a.b[1], a.b[2]};
+  const uint32_t* hw[3] = {a.shw[0], a.shw[1], a.shw[2]};
+  const void* hs[3] = {a.shs[0], a.shs[1], a.shs[2]};
+  const void* hb[3] = {a.shb[0], a.shb[1], a.shb[2]};
+  int64_t wst[3] = {a.wst[0], a.wst[1], a.wst[2]};
+  int64_t sst[3] = {a.sst[0], a.sst[1], a.sst[2]};
+#pragma unroll
+  for (int m = 0; m < 3; ++m) {
+    ZMOE_PIN(mw[m]); ZMOE_PIN(ms[m]); ZMOE_PIN(mb[m]); ZMOE_PIN(hw[m]); ZMOE_PIN(hs[m]); ZMOE_PIN(hb[m]);
+    ZMOE_PIN(wst[m]); ZMOE_PIN(sst[m]);
+  }
+  uint32_t* act = a.act;
+  uint32_t* xy = a.xy;
+  uint16_t* out = a.out;
+  uint32_t* out_idx = a.out_idx;
+  float* out_w = a.out_w;
+  unsigned long long* trace = a.trace;
+  int cmode = a.combine_mode, act_stride = a.act_stride, rkind = a.route_kind, norm = a.norm, wbf = a.w_bf16;
+  ZMOE_PIN(act); ZMOE_PIN(xy); ZMOE_PIN(out); ZMOE_PIN(out_idx); ZMOE_PIN(out_w); ZMOE_PIN(trace);
+  ZMOE_PIN(cmode); ZMOE_PIN(act_stride); ZMOE_PIN(rkind); ZMOE_PIN(norm); ZMOE_PIN(wbf);
+
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = __lane_id();
   // the workgroups on physical XCD `xcd` (g, g + 8, g + 16, ...) compute unit
@@ -103,7 +205,6 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(FusedParams p) {
   const int xcd = xcc_id();
   const int gi = blockIdx.x / kNX;
   const int q = gi * kFWaves + wave;  // wave index within the XCD
-  const int E = p.E, K = p.K;
   const AffineK ak = affine_k();
 
   // phase stamps of thread 0, kept in registers and stored at the end
@@ -111,25 +212,29 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(FusedParams p) {
 #pragma unroll
   for (int i = 0; i < kTraceSlots; ++i) tsr[i] = 0;
   auto mark = [&](int i) {
-    if (p.trace) tsr[i] = wall_clock64();
+    if (trace) tsr[i] = wall_clock64();
+  };
+  auto timeout = [&]() {
+    __hip_atomic_fetch_or((ZMOE_GLOBAL unsigned*)(sync + kErrWord), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
   mark(0);
-  const unsigned epoch = dev_load(p.sync + kEpochWord + blockIdx.x);
+  const unsigned epoch = dev_load(sync + kEpochWord + blockIdx.x);
   const unsigned tag16 = (epoch + 1u) & 0xFFFFu;
+  bool dead = false;  // a wait of this thread gave up (later waits give up at once)
 
   // ---------------- R: router logits, XCD-local ----------------
-  uint32_t* lg = reinterpret_cast<uint32_t*>(p.rpart) + E * (1 + xcd);
+  uint32_t* lg = lg0 + E * (1 + xcd);
   {
     // x in registers: lane l holds elements 8 l .. 8 l + 7 of each 512-chunk
     uint4 xv[S::NC];
 #pragma unroll
-    for (int c = 0; c < S::NC; ++c) xv[c] = gload(reinterpret_cast<const uint4*>(p.x + c * 512 + lane * 8));
+    for (int c = 0; c < S::NC; ++c) xv[c] = gload(reinterpret_cast<const uint4*>(x + c * 512 + lane * 8));
     for (int u = q; u < E; u += kXWX) {
       uint4 wv[S::NC];
 #pragma unroll
       for (int c = 0; c < S::NC; ++c)
-        wv[c] = gload(reinterpret_cast<const uint4*>(p.wr + static_cast<int64_t>(u) * kXH + c * 512 + lane * 8));
-      float a = 0.0f;
+        wv[c] = gload(reinterpret_cast<const uint4*>(wr + static_cast<int64_t>(u) * kXH + c * 512 + lane * 8));
+      float acc = 0.0f;
 #pragma unroll
       for (int c = 0; c < S::NC; ++c) {
         float d = 0.0f;
@@ -137,10 +242,10 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(FusedParams p) {
         d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv[c].y), __builtin_bit_cast(bf16x2_t, xv[c].y), d, false);
         d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv[c].z), __builtin_bit_cast(bf16x2_t, xv[c].z), d, false);
         d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, wv[c].w), __builtin_bit_cast(bf16x2_t, xv[c].w), d, false);
-        a += wave_sum(d);  // chunks in order
+        acc += wave_sum(d);  // chunks in order
       }
       // an ordinary store: the word stays in this XCD's L2 for its readers
-      if (lane == 0) gstore(lg + u, (tag16 << 16) | f32_to_bf16_bits(a));
+      if (lane == 0) gstore(lg + u, (tag16 << 16) | f32_to_bf16_bits(acc));
     }
     // wave 0 writes the x tile in stage_rows_lds's layout: item (segment
     // c * 16 + l / 4, quarter l % 4); each lane forms its segment's sum in A
@@ -172,8 +277,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(FusedParams p) {
     RowVals<P> row;
     for (unsigned n = 0;; ++n) {
       uint32_t wd[P];
-#pragma unroll
-      for (int i = 0; i < P; ++i) wd[i] = dev_load(lg + min(lane + 64 * i, E - 1));
+      xcd_load_row<P>(lg, E, wd);
       bool ok = true;
 #pragma unroll
       for (int i = 0; i < P; ++i) {
@@ -181,14 +285,15 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(FusedParams p) {
         row.v[i] = lane + 64 * i < E ? bf16_bits_to_f32(wd[i] & 0xFFFFu) : -INFINITY;
       }
       if (__all(ok)) break;
-      if (n > kSpinLimit) {
-        if (lane == 0) wait_timeout(p);
+      if (n > kXSpinLimit) {
+        if (lane == 0) timeout();
+        dead = true;
         break;
       }
     }
     mark(3);
     float(&v)[P] = row.v;
-    if (p.route.kind == kRouteSoftmaxProbs) {
+    if (rkind == kRouteSoftmaxProbs) {
       // moe_mlp.py:255-266: precise softmax, probabilities rounded to bf16
       const float m = reg_row_max(v, E);
 #pragma unroll
@@ -215,14 +320,6 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(FusedParams p) {
       const uint32_t u16 = (ok & 0x8000u) ? (ok & 0x7FFFu) : (~ok & 0xFFFFu);
       L.route.sel[r] = i;
       L.route.sval[r] = __uint_as_float(u16 << 16);
-      if (r == xcd) {
-#pragma unroll
-        for (int m = 0; m < 3; ++m) set_unit_e(p, L, 0, m, i);
-      }
-    }
-    if (K == xcd && threadIdx.x == kFThreads - 1) {  // the shared expert's XCD
-#pragma unroll
-      for (int m = 0; m < 3; ++m) set_unit_e(p, L, 0, m, -1);
     }
   }
   mark(4);
@@ -230,30 +327,59 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(FusedParams p) {
   mark(5);
 
   // ---------------- A: gate/up + SwiGLU of unit xcd ----------------
+  // this XCD's unit: the expert of rank xcd, or the shared expert (unit K)
+  const int ue = xcd < K ? __builtin_amdgcn_readfirstlane(L.route.sel[xcd]) : -1;
+  const uint32_t* uw[3];
+  const void* us[3];
+  const void* ub[3];
+#pragma unroll
+  for (int m = 0; m < 3; ++m) {
+    uw[m] = ue >= 0 ? mw[m] + ue * wst[m] : hw[m];
+    us[m] = ue >= 0 ? static_cast<const void*>(static_cast<const char*>(ms[m]) + ue * sst[m]) : hs[m];
+    ub[m] = ue >= 0 ? (mb[m] ? static_cast<const void*>(static_cast<const char*>(mb[m]) + ue * sst[m]) : nullptr) : hb[m];
+  }
   // The gate/up rows are loaded first and alone; each wave loads its
   // down-projection items once its gate/up rows have arrived, so the act
   // rows are not queued behind down-projection bytes.
   constexpr int64_t wpr = kXH / 8;
-  const int ppr = (QMODE == ZMOE_Q_AFFINE) ? (S::S_H >> p.gshift) : S::S_H;
-  const int pi = (QMODE == ZMOE_Q_AFFINE) ? (lane >> p.gshift) : lane;
+  const int ppr = (QMODE == ZMOE_Q_AFFINE) ? (S::S_H >> gshift) : S::S_H;
+  const int pi = (QMODE == ZMOE_Q_AFFINE) ? (lane >> gshift) : lane;
   const int a_r0 = q * S::RA;  // gate/up rows [a_r0, a_r0 + RA)
   uint4 wg[S::RA], wu[S::RA];
   RawParam rg[S::RA], ru[S::RA];
-  {
-    const uint32_t* gw = L.w[0][0] + lane * 4;
-    const uint32_t* uw = L.w[1][0] + lane * 4;
-    const void *gs = L.s[0][0], *gb = L.b[0][0], *us = L.s[1][0], *ub = L.b[1][0];
 #pragma unroll
-    for (int j = 0; j < S::RA; ++j) {
-      const int r = min(a_r0 + j, I_ - 1);  // past the last row: repeat it
-      wg[j] = gload(reinterpret_cast<const uint4*>(gw + r * wpr));
-      wu[j] = gload(reinterpret_cast<const uint4*>(uw + r * wpr));
-      rg[j] = seg_param_load<QMODE>(gs, gb, r * ppr + pi);
-      ru[j] = seg_param_load<QMODE>(us, ub, r * ppr + pi);
-    }
+  for (int j = 0; j < S::RA; ++j) {
+    const int r = min(a_r0 + j, I_ - 1);  // past the last row: repeat it
+    wg[j] = gload(reinterpret_cast<const uint4*>(uw[0] + r * wpr + lane * 4));
+    wu[j] = gload(reinterpret_cast<const uint4*>(uw[1] + r * wpr + lane * 4));
+    rg[j] = seg_param_load<QMODE>(us[0], ub[0], r * ppr + pi);
+    ru[j] = seg_param_load<QMODE>(us[1], ub[1], r * ppr + pi);
   }
   mark(13);
-  if (wave == 0) rank_weights(p, L, K);
+  // gate weights of the ranked winners (wave 0, lane r = winner r), for the
+  // combine, and the routing outputs of workgroup 0
+  if (wave == 0) {
+    const float val = lane < K ? L.route.sval[lane] : 0.0f;
+    float w;
+    if (rkind == kRouteSoftmaxProbs) {
+      const float sb = round_bf16(ordered_lane_sum(val, K));
+      w = norm ? div_to_bf16(val, sb) : val;
+    } else {
+      // moe.topk_gating_softmax renorm path (moe.py:1239-1396)
+      const float m = readlane_f(val, 0);
+      const float ex = expf(val - m);
+      const float sum = ordered_lane_sum(ex, K);
+      w = ex / sum;
+      if (wbf) w = round_bf16(w);
+    }
+    if (lane < K) {
+      L.route.w[lane] = w;
+      if (blockIdx.x == 0) {
+        if (out_idx) gstore(out_idx + lane, static_cast<uint32_t>(L.route.sel[lane]));
+        if (out_w) gstore(out_w + lane, w);
+      }
+    }
+  }
   uint32_t actw;
   {
     const uint4 x0 = *reinterpret_cast<const uint4*>(xs + ((0 * S::S_H) + lane) * 4);
@@ -294,51 +420,96 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(FusedParams p) {
   const int h0 = q * S::RD;
   const int rsD = lane / S::LI, liD = lane % S::LI;
   constexpr int64_t wprD = I_ / 8;
-  const int pprD = (QMODE == ZMOE_Q_AFFINE) ? (S::S_I >> p.gshift) : S::S_I;
+  const int pprD = (QMODE == ZMOE_Q_AFFINE) ? (S::S_I >> gshift) : S::S_I;
   uint4 wd[S::ND];
   RawParam rd[S::ND];
-  {
-    const uint32_t* dw = L.w[2][0];
-    const void *ds = L.s[2][0], *db = L.b[2][0];
 #pragma unroll
-    for (int j = 0; j < S::ND; ++j) {
-      const int g = j / S::TD, t = j % S::TD;
-      const int row = h0 + min(g * S::RPID + rsD, S::RD - 1);
-      const int s = t * S::LI + liD;
-      wd[j] = gload(reinterpret_cast<const uint4*>(dw + row * wprD + s * 4));
-      rd[j] = seg_param_load<QMODE>(ds, db, row * pprD + ((QMODE == ZMOE_Q_AFFINE) ? (s >> p.gshift) : s));
-    }
+  for (int j = 0; j < S::ND; ++j) {
+    const int g = j / S::TD, t = j % S::TD;
+    const int row = h0 + min(g * S::RPID + rsD, S::RD - 1);
+    const int sgm = t * S::LI + liD;
+    wd[j] = gload(reinterpret_cast<const uint4*>(uw[2] + row * wprD + sgm * 4));
+    rd[j] = seg_param_load<QMODE>(us[2], ub[2], row * pprD + ((QMODE == ZMOE_Q_AFFINE) ? (sgm >> gshift) : sgm));
   }
-  if (lane < S::RA && a_r0 + lane < I_) gstore(p.act + static_cast<int64_t>(xcd) * p.act_stride + a_r0 + lane, actw);
+  if (lane < S::RA && a_r0 + lane < I_) gstore(act + static_cast<int64_t>(xcd) * act_stride + a_r0 + lane, actw);
   mark(7);
 
   // ---------------- D: the unit's act row from L2, down projection ----------------
-  stage_rows_lds<QMODE, true>(p, p.act + static_cast<int64_t>(xcd) * p.act_stride, p.act_stride, 1, S::S_I, as, asx,
-                              tag16, p.by_S4I, p.by_SI);
+  // stage the act row in LDS in stage_rows_lds's layout: item i = (segment
+  // i / 4, quarter i % 4), 8 tagged words, polled until every tag is current
+  {
+    constexpr int NI = S::S_I * 4;
+    static_assert(NI <= kFThreads, "one staged item per thread");
+    if (threadIdx.x < NI) {
+      const int i = threadIdx.x;
+      const uint32_t* src = act + static_cast<int64_t>(xcd) * act_stride + i * 8;
+      const uint32_t want = tag16 << 16;
+      auto current = [&](const uint4& c) {
+        return ((c.x & 0xFFFF0000u) == want) && ((c.y & 0xFFFF0000u) == want) && ((c.z & 0xFFFF0000u) == want) &&
+               ((c.w & 0xFFFF0000u) == want);
+      };
+      uint4 w0, w1;
+      for (unsigned spins = 0;; ++spins) {
+        xcd_load_2x128(src, w0, w1);
+        if ((current(w0) && current(w1)) || dead) break;
+        if (spins > kXSpinLimit) {
+          timeout();
+          dead = true;
+          break;
+        }
+      }
+      auto pair = [](uint32_t lo, uint32_t hi) { return (lo & 0xFFFFu) | (hi << 16); };
+      const uint4 v = make_uint4(pair(w0.x, w0.y), pair(w0.z, w0.w), pair(w1.x, w1.y), pair(w1.z, w1.w));
+      uint4 o = v;
+      if (QMODE == ZMOE_Q_AFFINE) {
+        o.x = (v.x & 0xFFFFu) | (v.z << 16);
+        o.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
+        o.z = (v.y & 0xFFFFu) | (v.w << 16);
+        o.w = (v.y >> 16) | (v.w & 0xFFFF0000u);
+      }
+      *reinterpret_cast<uint4*>(as + ((i & 3) * S::S_I + (i >> 2)) * 4) = o;
+    }
+    if (QMODE == ZMOE_Q_AFFINE) {
+      lds_barrier();
+      if (threadIdx.x < S::S_I) {
+        const int sg = threadIdx.x;
+        float acc = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint4 o = *reinterpret_cast<const uint4*>(as + (w * S::S_I + sg) * 4);
+          acc += bf16_bits_to_f32(o.x & 0xFFFFu) + bf16_bits_to_f32(o.y & 0xFFFFu);
+          acc += bf16_bits_to_f32(o.z & 0xFFFFu) + bf16_bits_to_f32(o.w & 0xFFFFu);
+          acc += bf16_bits_to_f32(o.x >> 16) + bf16_bits_to_f32(o.y >> 16);
+          acc += bf16_bits_to_f32(o.z >> 16) + bf16_bits_to_f32(o.w >> 16);
+        }
+        asx[sg] = acc;
+      }
+    }
+  }
   mark(8);
   lds_barrier();
   mark(9);
-  float ysum[S::ND];
   {
+    float ysum[S::ND];
     float acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < S::ND; ++j) {
       const int t = j % S::TD;
-      const int s = t * S::LI + liD;
+      const int sgm = t * S::LI + liD;
       float sdj, cdj;
       seg_param_decode<QMODE>(rd[j], sdj, cdj);
-      const float xsum = (QMODE == ZMOE_Q_AFFINE) ? asx[s] : 0.0f;
-      acc = seg_accum<QMODE>(t == 0 ? 0.0f : acc, sdj, cdj, seg_dot_lds<QMODE>(wd[j], as, S::S_I, 0, s, ak), xsum);
+      const float xsum = (QMODE == ZMOE_Q_AFFINE) ? asx[sgm] : 0.0f;
+      acc = seg_accum<QMODE>(t == 0 ? 0.0f : acc, sdj, cdj, seg_dot_lds<QMODE>(wd[j], as, S::S_I, 0, sgm, ak), xsum);
       ysum[j] = (t == S::TD - 1) ? wave_sum_width<S::LI>(acc) : 0.0f;
     }
-  }
-  mark(11);
+    mark(11);
 #pragma unroll
-  for (int j = 0; j < S::ND; ++j) {
-    const int g = j / S::TD, t = j % S::TD;
-    const int hl = g * S::RPID + rsD;
-    if (t == S::TD - 1 && liD == 0 && hl < S::RD)
-      dev_store(p.xy + static_cast<int64_t>(xcd) * kXH + h0 + hl, (tag16 << 16) | f32_to_bf16_bits(ysum[j]));
+    for (int j = 0; j < S::ND; ++j) {
+      const int g = j / S::TD, t = j % S::TD;
+      const int hl = g * S::RPID + rsD;
+      if (t == S::TD - 1 && liD == 0 && hl < S::RD)
+        dev_store(xy + static_cast<int64_t>(xcd) * kXH + h0 + hl, (tag16 << 16) | f32_to_bf16_bits(ysum[j]));
+    }
   }
   mark(10);
 
@@ -349,13 +520,13 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(FusedParams p) {
   if (xcd == gi % kNX) {
     const int k = lane / S::RD, r = lane % S::RD;
     const bool mine = k < kNX;
-    const uint32_t* src = p.xy + static_cast<int64_t>(mine ? k : 0) * kXH + h0 + r;
+    const uint32_t* src = xy + static_cast<int64_t>(mine ? k : 0) * kXH + h0 + r;
     uint32_t v = 0;
     for (unsigned spins = 0;; ++spins) {
       v = dev_load(src);
-      if (__all(!mine || (v >> 16) == tag16)) break;
-      if (spins > kSpinLimit) {
-        if (lane == 0) wait_timeout(p);
+      if (__all(!mine || (v >> 16) == tag16) || dead) break;
+      if (spins > kXSpinLimit) {
+        if (lane == 0) timeout();
         break;
       }
     }
@@ -365,18 +536,18 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(FusedParams p) {
     if (lane < S::RD) {
       const float* yr = yw + lane * kNX;
       const float* wk = L.route.w;
-      float o = round_bf16(combine_one(p.combine_mode, K, [&](int kk) { return yr[kk]; }, [&](int kk) { return wk[kk]; }));
+      float o = round_bf16(combine_one(cmode, K, [&](int kk) { return yr[kk]; }, [&](int kk) { return wk[kk]; }));
       if (K < kNX) o = add_nofma(o, yr[K]);
-      gstore(p.out + h0 + lane, static_cast<uint16_t>(f32_to_bf16_bits(o)));
+      gstore(out + h0 + lane, static_cast<uint16_t>(f32_to_bf16_bits(o)));
     }
   }
   mark(12);
   if (threadIdx.x == 0) {
-    dev_store(p.sync + kEpochWord + blockIdx.x, epoch + 1);
-    if (p.trace) {
+    dev_store(sync + kEpochWord + blockIdx.x, epoch + 1);
+    if (trace) {
 #pragma unroll
       for (int i = 0; i < kTraceSlots; ++i)
-        if (tsr[i]) gstore(p.trace + blockIdx.x * kTraceSlots + i, tsr[i]);
+        if (tsr[i]) gstore(trace + blockIdx.x * kTraceSlots + i, tsr[i]);
     }
   }
 }
@@ -451,7 +622,7 @@ static bool d1x_shape_ok(const zmoe_layer_desc* d, int G) {
 }
 
 template <int QMODE, int P, int I_>
-static int launch_d1x_t(hipStream_t st, const FusedParams& fp) {
+static int launch_d1x_t(hipStream_t st, const D1XArgs& a) {
   static bool prepared = false;
   const void* fn = reinterpret_cast<const void*>(&k_moe_decode1x<QMODE, P, I_>);
   const size_t lds = d1x_lds_bytes(I_);
@@ -462,36 +633,60 @@ static int launch_d1x_t(hipStream_t st, const FusedParams& fp) {
   int occ = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, kFThreads, lds) != hipSuccess || occ < 1)
     return fail(ZMOE_EUNSUPPORTED, "[moe_layer] XCD-partitioned kernel cannot be resident on every CU");
-  hipLaunchKernelGGL((k_moe_decode1x<QMODE, P, I_>), dim3(kXG), dim3(kFThreads), lds, st, fp);
+  hipLaunchKernelGGL((k_moe_decode1x<QMODE, P, I_>), dim3(kXG), dim3(kFThreads), lds, st, a);
   return check_launch("moe_layer(XCD-partitioned one-token launch)");
 }
 
 template <int QMODE, int I_>
-static int launch_d1x_p(hipStream_t st, const FusedParams& fp) {
-  switch (route_slots(fp.E)) {
-    case 1: return launch_d1x_t<QMODE, 1, I_>(st, fp);
-    case 2: return launch_d1x_t<QMODE, 2, I_>(st, fp);
-    default: return launch_d1x_t<QMODE, 4, I_>(st, fp);
+static int launch_d1x_p(hipStream_t st, const D1XArgs& a) {
+  switch (route_slots(a.E)) {
+    case 1: return launch_d1x_t<QMODE, 1, I_>(st, a);
+    case 2: return launch_d1x_t<QMODE, 2, I_>(st, a);
+    default: return launch_d1x_t<QMODE, 4, I_>(st, a);
   }
 }
 
 template <int QMODE>
-static int launch_d1x_q(hipStream_t st, const FusedParams& fp) {
-  return fp.I == 768 ? launch_d1x_p<QMODE, 768>(st, fp) : launch_d1x_p<QMODE, 1024>(st, fp);
+static int launch_d1x_q(hipStream_t st, const D1XArgs& a, int I) {
+  return I == 768 ? launch_d1x_p<QMODE, 768>(st, a) : launch_d1x_p<QMODE, 1024>(st, a);
 }
 
-int try_decode1x(hipStream_t st, const zmoe_layer_desc* d, const FusedParams& fp_in, int grid) {
-  if (!d1x_shape_ok(d, grid) || fp_in.xy == nullptr) return -1;
-  if (!xcd_round_robin(st, fp_in.xy, grid)) return -1;
-  FusedParams fp = fp_in;
+int try_decode1x(hipStream_t st, const zmoe_layer_desc* d, const FusedParams& fp, int grid) {
+  if (!d1x_shape_ok(d, grid) || fp.xy == nullptr) return -1;
+  if (!xcd_round_robin(st, fp.xy, grid)) return -1;
+  D1XArgs a{};
+  a.x = fp.x;
+  a.out = fp.out;
+  a.wr = fp.wr;
   for (int m = 0; m < 3; ++m) {
+    a.w[m] = fp.w[m];
+    a.s[m] = fp.s[m];
+    a.b[m] = fp.b[m];
+    a.shw[m] = fp.w[3 + m];
+    a.shs[m] = fp.s[3 + m];
+    a.shb[m] = fp.b[3 + m];
     const int64_t N = (m == 2) ? d->hidden : d->inter, Kin = (m == 2) ? d->inter : d->hidden;
     const int64_t groups = (d->quant_mode == ZMOE_Q_AFFINE) ? Kin / d->group_size : Kin / 32;
-    fp.d1.wst[m] = N * (Kin / 8);
-    fp.d1.sst[m] = N * groups * ((d->quant_mode == ZMOE_Q_AFFINE) ? 2 : 1);
+    a.wst[m] = N * (Kin / 8);
+    a.sst[m] = N * groups * ((d->quant_mode == ZMOE_Q_AFFINE) ? 2 : 1);
   }
-  if (d->quant_mode == ZMOE_Q_AFFINE) return launch_d1x_q<ZMOE_Q_AFFINE>(st, fp);
-  return launch_d1x_q<ZMOE_Q_MXFP4>(st, fp);
+  a.sync = fp.sync;
+  a.lg = reinterpret_cast<uint32_t*>(fp.rpart);
+  a.act = fp.act;
+  a.xy = fp.xy;
+  a.out_idx = fp.out_idx;
+  a.out_w = fp.out_w;
+  a.trace = fp.trace;
+  a.E = fp.E;
+  a.K = fp.K;
+  a.gshift = fp.gshift;
+  a.combine_mode = fp.combine_mode;
+  a.act_stride = fp.act_stride;
+  a.route_kind = fp.route.kind;
+  a.norm = fp.route.norm;
+  a.w_bf16 = fp.route.w_bf16;
+  if (d->quant_mode == ZMOE_Q_AFFINE) return launch_d1x_q<ZMOE_Q_AFFINE>(st, a, d->inter);
+  return launch_d1x_q<ZMOE_Q_MXFP4>(st, a, d->inter);
 }
 
 }  // namespace zmoe
