@@ -338,6 +338,24 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
     us[m] = ue >= 0 ? static_cast<const void*>(static_cast<const char*>(ms[m]) + ue * sst[m]) : hs[m];
     ub[m] = ue >= 0 ? (mb[m] ? static_cast<const void*>(static_cast<const char*>(mb[m]) + ue * sst[m]) : nullptr) : hb[m];
   }
+  // down-projection items: lane group rs (of RPID) takes row h0 + g * RPID +
+  // rs, lane li of it segments t * LI + li
+  const int h0 = q * S::RD;
+  const int rsD = lane / S::LI, liD = lane % S::LI;
+  constexpr int64_t wprD = I_ / 8;
+  const int pprD = (QMODE == ZMOE_Q_AFFINE) ? (S::S_I >> gshift) : S::S_I;
+  uint4 wd[S::ND];
+  RawParam rd[S::ND];
+  auto load_d = [&]() {
+#pragma unroll
+    for (int j = 0; j < S::ND; ++j) {
+      const int g = j / S::TD, t = j % S::TD;
+      const int row = h0 + min(g * S::RPID + rsD, S::RD - 1);
+      const int sgm = t * S::LI + liD;
+      wd[j] = gload(reinterpret_cast<const uint4*>(uw[2] + row * wprD + sgm * 4));
+      rd[j] = seg_param_load<QMODE>(us[2], ub[2], row * pprD + ((QMODE == ZMOE_Q_AFFINE) ? (sgm >> gshift) : sgm));
+    }
+  };
   // The gate/up rows are loaded first and alone; each wave loads its
   // down-projection items once its gate/up rows have arrived, so the act
   // rows are not queued behind down-projection bytes.
@@ -415,22 +433,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
     actw = (tag16 << 16) | swiglu_bf16(round_bf16(gsel), round_bf16(usel));
   }
   mark(6);
-  // down-projection items: lane group rs (of RPID) takes row h0 + g * RPID +
-  // rs, lane li of it segments t * LI + li
-  const int h0 = q * S::RD;
-  const int rsD = lane / S::LI, liD = lane % S::LI;
-  constexpr int64_t wprD = I_ / 8;
-  const int pprD = (QMODE == ZMOE_Q_AFFINE) ? (S::S_I >> gshift) : S::S_I;
-  uint4 wd[S::ND];
-  RawParam rd[S::ND];
-#pragma unroll
-  for (int j = 0; j < S::ND; ++j) {
-    const int g = j / S::TD, t = j % S::TD;
-    const int row = h0 + min(g * S::RPID + rsD, S::RD - 1);
-    const int sgm = t * S::LI + liD;
-    wd[j] = gload(reinterpret_cast<const uint4*>(uw[2] + row * wprD + sgm * 4));
-    rd[j] = seg_param_load<QMODE>(us[2], ub[2], row * pprD + ((QMODE == ZMOE_Q_AFFINE) ? (sgm >> gshift) : sgm));
-  }
+  load_d();
   if (lane < S::RA && a_r0 + lane < I_) gstore(act + static_cast<int64_t>(xcd) * act_stride + a_r0 + lane, actw);
   mark(7);
 
