@@ -120,6 +120,21 @@ def test_mixtral_matches_lfm2_does_not():
     assert P.find_moe_blocks(small) == []
 
 
+def test_qwen2_moe_gated_shared_expert_not_matched():
+    """Qwen2-MoE blocks add a sigmoid-gated shared expert that the routed
+    layer does not compute; swapping them would drop that term, so neither
+    pattern may take them."""
+    from transformers import Qwen2MoeConfig
+    from transformers.models.qwen2_moe.modeling_qwen2_moe import Qwen2MoeSparseMoeBlock
+
+    blk = Qwen2MoeSparseMoeBlock(Qwen2MoeConfig(hidden_size=H, moe_intermediate_size=I, num_experts=E,
+                                                num_experts_per_tok=K, shared_expert_intermediate_size=I))
+    assert hasattr(blk, "shared_expert") and hasattr(blk, "shared_expert_gate")
+    assert P.find_moe_blocks(blk) == []
+    out = P.patch(blk, device=torch.device("cpu"))
+    assert out._zmlx_patch_result.patched == [] and blk.__class__ is Qwen2MoeSparseMoeBlock
+
+
 def test_patch_selection_and_errors():
     m = _qwen3_model(layers=2)
     # host-resident weights: each block's apply fails, is recorded, and the

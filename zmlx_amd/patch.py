@@ -171,6 +171,8 @@ class MoEMLPPattern(PatchPattern):
             return False
         if hasattr(gate, "e_score_correction_bias") or hasattr(module, "shared_experts"):
             return False  # sigmoid routers: deepseek_router
+        if hasattr(module, "shared_expert") or hasattr(module, "shared_expert_gate"):
+            return False  # Qwen2-MoE: a sigmoid-gated shared expert the routed-only layer would drop
         if getattr(module, "use_expert_bias", False) or hasattr(gate, "routed_scaling_factor"):
             return False  # sigmoid + bias routers this pattern does not cover
         return _shapes_supported(module)
