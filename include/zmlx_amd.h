@@ -56,7 +56,8 @@ extern "C" {
 #define ZMOE_ROUTER_TOPK_LOGITS 1    /* moe.topk_gating_softmax fast path: top-k logits, softmax over k */
 #define ZMOE_ROUTER_SIGMOID_GROUPED 2 /* DeepSeek/GLM: sigmoid + bias, grouped top-k */
 
-/* Library version string, e.g. "zmlx_amd 0.1.0 gfx950". */
+/* Library version string, e.g. "zmlx_amd 0.1.0 gfx950 src:0123456789abcdef": the
+ * version, the target and a hash of the sources the library was built from. */
 const char* zmoe_version(void);
 
 /* Message of the last failed call on this thread ("" if none). */

@@ -31,6 +31,25 @@ def test_version(lib):
     assert v.startswith("zmlx_amd ") and "gfx950" in v
 
 
+def _check_built_from_tree():
+    from zmlx_amd.build import source_hash
+
+    v = N.version()
+    assert v.endswith(f"src:{source_hash()}"), f"loaded library ({v}) was not built from these sources"
+
+
+def test_library_built_from_this_tree(lib):
+    _check_built_from_tree()
+
+
+@pytest.mark.gpu
+def test_gpu_library_built_from_this_tree():
+    """On the GPU box: the mapped library carries the hash of the sources it
+    runs next to."""
+    N.lib()
+    _check_built_from_tree()
+
+
 def _qmm_swiglu(lib, **kw):
     a = dict(stream=None, x=None, x_batch=1, gw=None, gs=None, gb=None, uw=None, us=None, ub=None, lhs=None,
              rhs=None, n_pairs=1, M=1, Nn=64, K=512, E=4, group_size=64, bits=4, quant_mode=N.Q_AFFINE, out=None)

@@ -8,6 +8,7 @@ source tree; nothing is installed elsewhere.
 from __future__ import annotations
 
 import concurrent.futures as cf
+import hashlib
 import os
 import shutil
 import subprocess
@@ -33,6 +34,20 @@ HIPCC_FLAGS = [
 ]
 
 
+def source_hash() -> str:
+    """Hash of the library's sources (csrc/*.hip, csrc/*.h and the public
+    header), compiled into zmoe_version() so a loaded library can be checked
+    against the tree it is loaded from."""
+    h = hashlib.sha256()
+    files = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.h")) + [INCLUDE / "zmlx_amd.h"]
+    for f in files:
+        h.update(f.name.encode())
+        h.update(b"\0")
+        h.update(f.read_bytes())
+        h.update(b"\0")
+    return h.hexdigest()[:16]
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -49,7 +64,7 @@ def _compile(src: Path, obj: Path, extra: list[str]) -> None:
 
 def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
     """Compile every HIP source and link the shared library; returns its path."""
-    extra = list(extra_flags or [])
+    extra = list(extra_flags or []) + [f'-DZMOE_SOURCE_HASH="{source_hash()}"']
     obj_dir = OUT_DIR / "obj"
     obj_dir.mkdir(parents=True, exist_ok=True)
     srcs = sorted(CSRC.glob("*.hip"))

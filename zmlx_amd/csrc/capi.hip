@@ -11,6 +11,12 @@ void set_error(const std::string& msg) { g_last_error = msg; }
 
 }  // namespace zmoe
 
-extern "C" const char* zmoe_version(void) { return "zmlx_amd 0.1.0 gfx950"; }
+#ifndef ZMOE_SOURCE_HASH
+#define ZMOE_SOURCE_HASH "unknown"
+#endif
+
+// "zmlx_amd <version> gfx950 src:<hash>", the hash of the sources the library
+// was built from (zmlx_amd/build.py source_hash()).
+extern "C" const char* zmoe_version(void) { return "zmlx_amd 0.1.0 gfx950 src:" ZMOE_SOURCE_HASH; }
 
 extern "C" const char* zmoe_last_error(void) { return zmoe::g_last_error.c_str(); }
