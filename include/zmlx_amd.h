@@ -63,6 +63,14 @@ const char* zmoe_version(void);
 /* Message of the last failed call on this thread ("" if none). */
 const char* zmoe_last_error(void);
 
+/* n zeroed words of page-locked host memory that kernels may store to and
+ * the host may read at any time (hipHostMalloc, mapped and coherent), for
+ * zmoe_layer_desc.error_flag_host; NULL on failure.  Free with
+ * zmoe_host_flags_free.  No counterpart in the reference (its kernels have
+ * no waits that can give up). */
+unsigned* zmoe_host_flags_alloc(int n);
+void zmoe_host_flags_free(unsigned* flags);
+
 /*
  * Fused gather + quantized GEMV + SwiGLU.
  * Replaces mx.gather_qmm_swiglu (integrations/mlx_local_integration/
@@ -217,6 +225,16 @@ typedef struct zmoe_layer_desc {
   const uint32_t* sh_up_w;   const void* sh_up_s;   const void* sh_up_b;
   const uint32_t* sh_down_w; const void* sh_down_s; const void* sh_down_b; /* [H, I_s/8] */
   int flags;                /* ZMOE_LAYER_* bits */
+  /* Single-launch kernels: when a wait for data exchanged between workgroups
+   * gives up, the kernel sets the workspace's sticky error word, writes NaN
+   * into the outputs that depend on the missing data, and stores 1 here if
+   * non-NULL (host-visible memory, e.g. hipHostMalloc), so that the host can
+   * notice without a synchronisation.  No counterpart in the reference
+   * (MLX kernels have no cross-workgroup waits). */
+  unsigned* error_flag_host;
+  /* Polls before such a wait gives up; 0 = the library's default.  Tests set
+   * it small to force the give-up path from the host. */
+  int spin_limit;
 } zmoe_layer_desc;
 
 /* zmoe_layer_desc.flags */
@@ -242,7 +260,8 @@ size_t zmoe_moe_layer_trace_info(const zmoe_layer_desc* desc, int B, int* n_bloc
  * and do not write it otherwise.  The single-launch kernel keeps a launch
  * count per workgroup in it and tags the data its workgroups exchange with
  * that count.  Bytes 128..131 hold a sticky error word: nonzero if a wait for
- * exchanged data timed out (zero-fill the workspace again before reuse). */
+ * exchanged data timed out; the outputs of that call are then NaN where they
+ * depend on the missing data (zero-fill the workspace again before reuse). */
 size_t zmoe_moe_layer_workspace_size(const zmoe_layer_desc* desc, int B);
 
 /*

@@ -331,3 +331,45 @@ def test_layer_expert_major_gemv(dev, mode, gs):
     idx = from_dev(idx).astype(np.int64)
     ref = _oracle_out(x, idx, O.bf16_round(from_dev(w)), banks, None, mode, gs, "native")
     _cmp_out(from_dev(out), ref)
+
+
+@pytest.mark.parametrize("family,shape,B", [
+    ("qwen3", dict(H=2048, E=32, I=768, K=8), 1),     # XCD-partitioned one-token kernel
+    ("lfm2", dict(H=2048, E=32, I=1792, K=4), 1),     # one-token kernel
+    ("qwen3", dict(H=2048, E=32, I=768, K=8), 4),     # batched kernel
+])
+def test_wait_give_up_is_loud(dev, family, shape, B):
+    """A single-launch kernel whose cross-workgroup wait gives up (forced from
+    the host with a spin limit of one poll, so every kernel still exits
+    normally) leaves NaN in the outputs it could not compute, sets the sticky
+    error word, and the next call raises ZmoeError.  Afterwards the layer
+    computes normally again (bit-identical to the kernel sequence)."""
+    import torch
+
+    from zmlx_amd import ZmoeError
+    from zmlx_amd import _native as N
+    from zmlx_amd.layer import QuantizedMoELayer
+
+    rng = np.random.default_rng(31)
+    banks, wr, sh, tq, tsh, wr_t = _build(dev, rng, **shape)
+    layer = QuantizedMoELayer.for_family(family, wr_t, tq["gate"], tq["up"], tq["down"], top_k=shape["K"])
+    assert layer._single_launch(B)
+    x = to_bf16(bf16_randn(rng, (B, shape["H"])), dev)
+    print(f"[give-up] {family} B={B}", flush=True)
+    layer.desc.spin_limit = 1
+    out = layer(x)
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).any(), "a wait that gave up left no NaN in the output"
+    assert layer.sync_error() != 0
+    assert layer._err_flag[0] == 1
+    layer.desc.spin_limit = 0
+    with pytest.raises(ZmoeError):
+        layer(x)
+    assert layer.sync_error() == 0  # the workspaces were cleared
+    got = layer(x)
+    layer.desc.flags |= N.LAYER_FORCE_MULTI
+    ref = layer(x)
+    layer.desc.flags &= ~N.LAYER_FORCE_MULTI
+    torch.cuda.synchronize()
+    assert layer.sync_error() == 0
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))

@@ -87,12 +87,16 @@ class LayerDesc(ctypes.Structure):
         ("sh_up_w", c_void_p), ("sh_up_s", c_void_p), ("sh_up_b", c_void_p),
         ("sh_down_w", c_void_p), ("sh_down_s", c_void_p), ("sh_down_b", c_void_p),
         ("flags", c_int),
+        ("error_flag_host", c_void_p),
+        ("spin_limit", c_int),
     ]
 
 
 _SIGNATURES = {
     "zmoe_version": (ctypes.c_char_p, []),
     "zmoe_last_error": (ctypes.c_char_p, []),
+    "zmoe_host_flags_alloc": (c_void_p, [c_int]),
+    "zmoe_host_flags_free": (None, [c_void_p]),
     "zmoe_gather_qmm_swiglu": (
         c_int,
         [c_void_p, c_void_p, c_i64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,

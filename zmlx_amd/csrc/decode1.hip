@@ -160,6 +160,7 @@ template <int QMODE, int P, bool XR>
 __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   D1Lds& L = *reinterpret_cast<D1Lds*>(smem);
+  wg_dead_clear();
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
   const int lane = __lane_id();
@@ -301,7 +302,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
           }
         }
         if (__all(ok)) break;
-        if (n > kSpinLimit) {
+        if (n > p.spin) {
           if (lane == 0) wait_timeout(p);
           break;
         }
@@ -530,7 +531,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
       }
       if (lane < kD1A && base + lane < g1)
         dev_store(p.act + static_cast<int64_t>(usel_u) * p.act_stride + rsel,
-                  (tag16 << 16) | swiglu_bf16(round_bf16(gsel), round_bf16(usel)));
+                  (tag16 << 16) | (wg_dead() ? kBf16NaN : swiglu_bf16(round_bf16(gsel), round_bf16(usel))));
     }
   } else {
     // general H: LH lanes per row (RPI rows per load), T segments per lane,
@@ -604,7 +605,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
             const float uv = lanes_sum(au, LH);
             if (li == 0)
               dev_store(p.act + static_cast<int64_t>(iu[b][j]) * p.act_stride + irow[b][j],
-                        (tag16 << 16) | swiglu_bf16(round_bf16(gv), round_bf16(uv)));
+                        (tag16 << 16) | (wg_dead() ? kBf16NaN : swiglu_bf16(round_bf16(gv), round_bf16(uv))));
           }
         }
       }
@@ -649,7 +650,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
     for (;;) {
       const bool ok = c >= kD1Ctrs || static_cast<int>(dev_load(p.aflag + c * kD1CtrStride) - target) >= 0;
       if (__all(ok)) break;
-      if (++spins > kSpinLimit) {
+      if (++spins > p.spin) {
         if (lane == 0) wait_timeout(p);
         break;
       }
@@ -721,6 +722,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
     const float* wk = L.route.w;
     float o = round_bf16(combine_one(p.combine_mode, K, [&](int k) { return yr[k]; }, [&](int k) { return wk[k]; }));
     if (has_shared) o = add_nofma(o, yr[K]);
+    if (wg_dead()) o = kPoison;
     gstore(p.out + h0 + lane, static_cast<uint16_t>(f32_to_bf16_bits(o)));
   }
   trace_mark(p, 12);

@@ -151,6 +151,8 @@ struct D1XArgs {
   uint32_t* out_idx;
   float* out_w;
   unsigned long long* trace;
+  unsigned* err_host;      // nullable host-visible flag, set when a wait gives up
+  unsigned spin;           // polls before a wait gives up
   int E, K, gshift, combine_mode, act_stride;
   int route_kind, norm, w_bf16;
 };
@@ -194,6 +196,9 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
   uint32_t* out_idx = a.out_idx;
   float* out_w = a.out_w;
   unsigned long long* trace = a.trace;
+  unsigned* err_host = a.err_host;
+  unsigned spin = a.spin;
+  ZMOE_PIN(err_host); ZMOE_PIN(spin);
   int cmode = a.combine_mode, act_stride = a.act_stride, rkind = a.route_kind, norm = a.norm, wbf = a.w_bf16;
   ZMOE_PIN(act); ZMOE_PIN(xy); ZMOE_PIN(out); ZMOE_PIN(out_idx); ZMOE_PIN(out_w); ZMOE_PIN(trace);
   ZMOE_PIN(cmode); ZMOE_PIN(act_stride); ZMOE_PIN(rkind); ZMOE_PIN(norm); ZMOE_PIN(wbf);
@@ -214,9 +219,8 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
   auto mark = [&](int i) {
     if (trace) tsr[i] = wall_clock64();
   };
-  auto timeout = [&]() {
-    __hip_atomic_fetch_or((ZMOE_GLOBAL unsigned*)(sync + kErrWord), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  };
+  auto timeout = [&]() { wait_timeout_at(sync, err_host); };
+  wg_dead_clear();
   mark(0);
   const unsigned epoch = dev_load(sync + kEpochWord + blockIdx.x);
   const unsigned tag16 = (epoch + 1u) & 0xFFFFu;
@@ -285,7 +289,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
         row.v[i] = lane + 64 * i < E ? bf16_bits_to_f32(wd[i] & 0xFFFFu) : -INFINITY;
       }
       if (__all(ok)) break;
-      if (n > kXSpinLimit) {
+      if (n > spin) {
         if (lane == 0) timeout();
         dead = true;
         break;
@@ -327,8 +331,10 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
   mark(5);
 
   // ---------------- A: gate/up + SwiGLU of unit xcd ----------------
-  // this XCD's unit: the expert of rank xcd, or the shared expert (unit K)
-  const int ue = xcd < K ? __builtin_amdgcn_readfirstlane(L.route.sel[xcd]) : -1;
+  // this XCD's unit: the expert of rank xcd, or the shared expert (unit K).
+  // Clamped: after a wait gave up, the waves may have ranked different
+  // (stale) logits, and then no thread need have written rank xcd.
+  const int ue = xcd < K ? min(max(__builtin_amdgcn_readfirstlane(L.route.sel[xcd]), 0), E - 1) : -1;
   const uint32_t* uw[3];
   const void* us[3];
   const void* ub[3];
@@ -430,7 +436,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
         usel = uv;
       }
     }
-    actw = (tag16 << 16) | swiglu_bf16(round_bf16(gsel), round_bf16(usel));
+    actw = (tag16 << 16) | (wg_dead() ? kBf16NaN : swiglu_bf16(round_bf16(gsel), round_bf16(usel)));
   }
   mark(6);
   load_d();
@@ -455,7 +461,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
       for (unsigned spins = 0;; ++spins) {
         xcd_load_2x128(src, w0, w1);
         if ((current(w0) && current(w1)) || dead) break;
-        if (spins > kXSpinLimit) {
+        if (spins > spin) {
           timeout();
           dead = true;
           break;
@@ -511,7 +517,8 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
       const int g = j / S::TD, t = j % S::TD;
       const int hl = g * S::RPID + rsD;
       if (t == S::TD - 1 && liD == 0 && hl < S::RD)
-        dev_store(xy + static_cast<int64_t>(xcd) * kXH + h0 + hl, (tag16 << 16) | f32_to_bf16_bits(ysum[j]));
+        dev_store(xy + static_cast<int64_t>(xcd) * kXH + h0 + hl,
+                  (tag16 << 16) | (wg_dead() ? kBf16NaN : f32_to_bf16_bits(ysum[j])));
     }
   }
   mark(10);
@@ -528,7 +535,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
     for (unsigned spins = 0;; ++spins) {
       v = dev_load(src);
       if (__all(!mine || (v >> 16) == tag16) || dead) break;
-      if (spins > kXSpinLimit) {
+      if (spins > spin) {
         if (lane == 0) timeout();
         break;
       }
@@ -541,6 +548,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
       const float* wk = L.route.w;
       float o = round_bf16(combine_one(cmode, K, [&](int kk) { return yr[kk]; }, [&](int kk) { return wk[kk]; }));
       if (K < kNX) o = add_nofma(o, yr[K]);
+      if (wg_dead()) o = kPoison;
       gstore(out + h0 + lane, static_cast<uint16_t>(f32_to_bf16_bits(o)));
     }
   }
@@ -680,6 +688,8 @@ int try_decode1x(hipStream_t st, const zmoe_layer_desc* d, const FusedParams& fp
   a.out_idx = fp.out_idx;
   a.out_w = fp.out_w;
   a.trace = fp.trace;
+  a.err_host = fp.err_host;
+  a.spin = d->spin_limit > 0 ? static_cast<unsigned>(d->spin_limit) : kXSpinLimit;
   a.E = fp.E;
   a.K = fp.K;
   a.gshift = fp.gshift;

@@ -36,6 +36,7 @@ constexpr int kDBCtrStride = 32;
 constexpr int kDBCtrEpoch = kDBCtrs * kDBCtrStride;
 
 struct DBLds {
+  unsigned dead, pad_[3];  // word 0 of every single-launch kernel's LDS (wg_dead_word)
   RouteLds route[kDBMaxB];
   int slot_of[1024];            // expert -> unit (or -1)
   int ulist[kDBMaxUnits];
@@ -163,7 +164,7 @@ __device__ __forceinline__ void poll_logits2(const FusedParams& p, const unsigne
       }
     }
     if (__all(ok)) break;
-    if (++n > kSpinLimit) {
+    if (++n > p.spin) {
       if (lane == 0) wait_timeout(p);
       break;
     }
@@ -174,6 +175,7 @@ template <int QMODE, int P, int TDM>
 __global__ __launch_bounds__(kFThreads) void k_moe_decodeb(FusedParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   DBLds& L = *reinterpret_cast<DBLds*>(smem);
+  wg_dead_clear();
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = __lane_id();
@@ -440,7 +442,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decodeb(FusedParams p) {
       if (lane < nt * kDBA) {
         const int tk = lane >> 2, j = lane & 3;
         dev_store(p.act + static_cast<int64_t>(p0 + tk) * p.act_stride + bt.row0 + j,
-                  (tag16 << 16) | __float_as_uint(astage[lane]));
+                  (tag16 << 16) | (wg_dead() ? kBf16NaN : __float_as_uint(astage[lane])));
       }
       wave_lds_sync();
     };
@@ -493,7 +495,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decodeb(FusedParams p) {
     for (;;) {
       const bool ok = c >= kDBCtrs || static_cast<int>(dev_load(p.aflag + c * kDBCtrStride) - target) >= 0;
       if (__all(ok)) break;
-      if (++spins > kSpinLimit) {
+      if (++spins > p.spin) {
         if (lane == 0) wait_timeout(p);
         break;
       }
@@ -575,6 +577,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decodeb(FusedParams p) {
     float o = round_bf16(combine_one(p.combine_mode, K, [&](int k) { return yr[L.pslot[b * K + k]]; },
                                      [&](int k) { return wk[k]; }));
     if (has_shared) o = add_nofma(o, yr[L.pslot[npairs + b]]);
+    if (wg_dead()) o = kPoison;
     gstore(p.out + static_cast<int64_t>(b) * H + hb + wave, static_cast<uint16_t>(f32_to_bf16_bits(o)));
   }
   trace_mark(p, 12);
@@ -659,7 +662,6 @@ int launch_decodeb(hipStream_t st, const zmoe_layer_desc* d, const FusedParams& 
   pl.TA = 1;
   pl.TD = S_I / LI;
   pl.PB = db_pass_slots(d, fp.B);
-  if (const char* e = getenv("ZMOE_DB_PB")) pl.PB = atoi(e) < pl.PB ? atoi(e) : pl.PB;
   pl.by_NC = make_fastdiv(static_cast<uint32_t>(H / 512));
   pl.by_W = make_fastdiv(static_cast<uint32_t>(W));
   pl.by_I = make_fastdiv(static_cast<uint32_t>(I));

@@ -71,6 +71,7 @@ template <int QMODE, int P>
 __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   FusedLds& L = *reinterpret_cast<FusedLds*>(smem);
+  wg_dead_clear();
   unsigned char* big = smem + ((sizeof(FusedLds) + 15) & ~static_cast<size_t>(15));
 
   const int wave = threadIdx.x / kWave;
@@ -325,7 +326,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
       }
       if (lane < kChunkA && base + lane < g1)
         dev_store(p.act + static_cast<int64_t>(psel) * p.act_stride + rsel,
-                  (tag16 << 16) | swiglu_bf16(round_bf16(gsel), round_bf16(usel)));
+                  (tag16 << 16) | (wg_dead() ? kBf16NaN : swiglu_bf16(round_bf16(gsel), round_bf16(usel))));
       // gate/up data is in and the act rows are on their way: start the down
       // stream (issued earlier it would compete with this phase's loads and
       // hold the stores back)
@@ -401,7 +402,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
               const float uv = lanes_sum(au[tk * kWave], LH);
               if (li == 0)
                 dev_store(p.act + static_cast<int64_t>(L.upairs[u][tk]) * p.act_stride + irow[j],
-                          (tag16 << 16) | swiglu_bf16(round_bf16(gv), round_bf16(uv)));
+                          (tag16 << 16) | (wg_dead() ? kBf16NaN : swiglu_bf16(round_bf16(gv), round_bf16(uv))));
             }
           }
         }
@@ -465,6 +466,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode(FusedParams p) {
       const float* yr = ybuf + r * Ptot + b * K;
       float o = round_bf16(combine_one(p.combine_mode, K, [&](int k) { return yr[k]; }, [&](int k) { return wk[k]; }));
       if (has_shared) o = add_nofma(o, ybuf[r * Ptot + P0 + b]);
+      if (wg_dead()) o = kPoison;
       gstore(p.out + static_cast<int64_t>(b) * p.H + h, static_cast<uint16_t>(f32_to_bf16_bits(o)));
     }
   }
@@ -618,6 +620,8 @@ int launch_fused(hipStream_t st, const zmoe_layer_desc* d, const void* x, int B,
   fp.out_idx = out_idx;
   fp.out_w = out_w;
   fp.trace = (d->flags & ZMOE_LAYER_TRACE) ? reinterpret_cast<unsigned long long*>(base + off_trace(d, B)) : nullptr;
+  fp.err_host = d->error_flag_host;
+  fp.spin = d->spin_limit > 0 ? static_cast<unsigned>(d->spin_limit) : kSpinLimit;
   fp.xy = B == 1 ? reinterpret_cast<uint32_t*>(base + off_xy(d, B)) : nullptr;
   fp.by_S4H = make_fastdiv(static_cast<uint32_t>(d->hidden / 8));
   fp.by_SH = make_fastdiv(static_cast<uint32_t>(d->hidden / 32));

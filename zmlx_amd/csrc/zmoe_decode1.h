@@ -17,6 +17,7 @@ constexpr int kD1RankMaxE = 256;  // parallel ranking for E <= this
 
 
 struct D1Lds {
+  unsigned dead, pad_[3];  // word 0 of every single-launch kernel's LDS (wg_dead_word)
   RouteLds route;
   // packed (bf16 order key << 16 | 0xFFFF - e); the grouped sigmoid
   // router's 64-bit keys use all of it

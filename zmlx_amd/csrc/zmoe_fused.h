@@ -18,7 +18,7 @@ constexpr int kFMaxB = 8;                 // tokens per call on the fused path
 constexpr int kFMaxUnits = kFMaxB * kMaxTopK + 1;
 constexpr int kChunkA = 4;                // (row-group, segment) items per batch, phase A
 constexpr int kChunkD = 4;                // (slot-group, segment) items per batch, phase D
-constexpr unsigned kSpinLimit = 1u << 21;
+constexpr unsigned kSpinLimit = 1u << 18;  // default polls before a wait gives up
 constexpr int kTraceSlots = 24;
 // words of the workspace's leading state block
 constexpr int kErrWord = static_cast<int>(kSyncErrorByte / 4);
@@ -59,11 +59,14 @@ struct FusedParams {
   float* out_w;
   unsigned long long* trace;  // nullable: [G][kTraceSlots] realtime stamps
   uint32_t* xy;          // XCD-partitioned one-token kernel: [8][H] tagged expert outputs (bf16 | tag << 16)
+  unsigned* err_host;    // nullable host-visible flag, set when a wait gives up
+  unsigned spin;         // polls before a wait gives up
   FastDiv by_S4H, by_SH, by_S4I, by_SI;  // staged-row items: S*4 and S per row
   D1Plan d1;
 };
 
 struct FusedLds {
+  unsigned dead, pad_[3];  // word 0 of every single-launch kernel's LDS (wg_dead_word)
   int ulist[kFMaxUnits];   // expert of each unit (slot order = expert order)
   int ucount[kFMaxUnits];
   int upairs[kFMaxUnits][kFMaxB];
@@ -76,9 +79,32 @@ __device__ __forceinline__ void trace_mark(const FusedParams& p, int slot) {
   if (p.trace && threadIdx.x == 0) gstore(p.trace + blockIdx.x * kTraceSlots + slot, static_cast<unsigned long long>(wall_clock64()));
 }
 
-__device__ __forceinline__ void wait_timeout(const FusedParams& p) {
-  __hip_atomic_fetch_or((ZMOE_GLOBAL unsigned*)(p.sync + kErrWord), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Word 0 of the dynamic LDS of every single-launch kernel (the first member
+// of its LDS struct): nonzero once a wait of the workgroup gave up.  Thread 0
+// clears it at the start; the data the workgroup publishes afterwards and its
+// outputs are NaN while it is set, so a failed exchange never yields a
+// silently wrong result.
+__device__ __forceinline__ ZMOE_LDS unsigned* wg_dead_word() {
+  extern __shared__ unsigned zmoe_dyn_lds[];
+  return (ZMOE_LDS unsigned*)zmoe_dyn_lds;
 }
+__device__ __forceinline__ void wg_dead_clear() {
+  if (threadIdx.x == 0) *wg_dead_word() = 0u;
+}
+__device__ __forceinline__ bool wg_dead() {
+  return __hip_atomic_load(wg_dead_word(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0u;
+}
+constexpr uint32_t kBf16NaN = 0x7FC0u;
+constexpr float kPoison = __builtin_nanf("");
+
+// A wait gave up: the sticky error word, the workgroup's flag, and the
+// host-visible flag if there is one.
+__device__ __forceinline__ void wait_timeout_at(unsigned* sync, unsigned* err_host) {
+  __hip_atomic_fetch_or((ZMOE_GLOBAL unsigned*)(sync + kErrWord), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_fetch_or(wg_dead_word(), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  if (err_host) __hip_atomic_store(err_host, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void wait_timeout(const FusedParams& p) { wait_timeout_at(p.sync, p.err_host); }
 
 // Router logits of one token, lane-strided (e = lane + 64 i): the H/512
 // partials of each expert, summed in chunk order once every one of them
@@ -113,7 +139,7 @@ __device__ __forceinline__ RowVals<P> poll_logits(const FusedParams& p, const un
       }
     }
     if (__all(ok)) break;
-    if (++n > kSpinLimit) {
+    if (++n > p.spin) {
       if (lane == 0) wait_timeout(p);
       break;
     }
@@ -176,7 +202,7 @@ __device__ __forceinline__ void stage_rows_lds(const FusedParams& p, const void*
 #pragma unroll
         for (int h = 0; h < NI; ++h) ok = ok && current(w[h][0]) && current(w[h][1]);
         if (ok) break;
-        if (++spins > kSpinLimit) {
+        if (++spins > p.spin) {
           wait_timeout(p);
           break;
         }

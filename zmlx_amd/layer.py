@@ -65,7 +65,15 @@ class QuantizedMoELayer:
     ``routed_scaling_factor`` (DeepSeek gate), expert bias
     (``expert_bias`` / ``e_score_correction_bias``).  ``single_launch=False``
     forces the multi-kernel sequence (the single persistent kernel is used
-    for decode batches whenever it applies)."""
+    for decode batches whenever it applies).
+
+    The single-launch kernels run one workgroup per CU and exchange data
+    between workgroups inside the launch, so they assume that all of their
+    workgroups are resident at once: run the layer on one stream, with no
+    other kernel occupying CUs of the GPU at the same time.  If that fails, a
+    wait gives up (after a bounded number of polls), the affected outputs are
+    NaN and the next call raises ``ZmoeError`` (``sync_error()`` reads the
+    sticky error word directly)."""
 
     def __init__(
         self,
@@ -140,9 +148,25 @@ class QuantizedMoELayer:
                 setattr(d, f"{name}_s", keep(p.scales))
                 setattr(d, f"{name}_b", keep(p.biases))
         d.flags = (0 if single_launch else N.LAYER_FORCE_MULTI) | (N.LAYER_TRACE if trace else 0)
+        # host-visible flag the single-launch kernels set when a wait for
+        # exchanged data gives up (their outputs are then NaN); checked at the
+        # next call without a synchronisation
+        self._lib = N.lib()  # fail loudly now if the library is missing
+        self._err_ptr = self._lib.zmoe_host_flags_alloc(1)
+        if not self._err_ptr:
+            raise N.ZmoeError("moe_layer: could not allocate the host-visible error flag")
+        self._err_flag = ctypes.cast(self._err_ptr, ctypes.POINTER(ctypes.c_uint))
+        d.error_flag_host = self._err_ptr
+        d.spin_limit = 0
         self.desc = d
         self._ws: dict[int, torch.Tensor] = {}
-        N.lib()  # fail loudly now if the library is missing
+        self._scratch: torch.Tensor | None = None
+
+    def __del__(self):
+        ptr, lib = getattr(self, "_err_ptr", None), getattr(self, "_lib", None)
+        if ptr and lib is not None:
+            lib.zmoe_host_flags_free(ptr)
+            self._err_ptr = None
 
     @classmethod
     def for_family(cls, family: str, *args, **kwargs) -> QuantizedMoELayer:
@@ -154,14 +178,38 @@ class QuantizedMoELayer:
     def workspace_bytes(self, B: int) -> int:
         return int(N.lib().zmoe_moe_layer_workspace_size(ctypes.byref(self.desc), int(B)))
 
+    def _single_launch(self, B: int) -> bool:
+        """Whether batch B runs a single-launch kernel (whose workspace keeps
+        launch counts from call to call)."""
+        nb, ns = ctypes.c_int(0), ctypes.c_int(0)
+        return int(N.lib().zmoe_moe_layer_trace_info(ctypes.byref(self.desc), int(B), ctypes.byref(nb),
+                                                          ctypes.byref(ns))) != 0
+
     def _workspace(self, B: int) -> torch.Tensor:
+        """Single-launch batches (at most 16 sizes) keep one zero-filled
+        workspace each: it holds launch counts that only grow from call to
+        call.  Every other batch shares one scratch buffer that grows to the
+        largest batch seen (the kernel sequence keeps nothing across calls)."""
         ws = self._ws.get(B)
-        if ws is None:
-            # zero-filled once: the leading block holds the fused kernel's
-            # launch counts (they only increase from call to call)
-            ws = torch.zeros(self.workspace_bytes(B), dtype=torch.uint8, device=self.device)
+        if ws is not None:
+            return ws
+        need = self.workspace_bytes(B)
+        if self._single_launch(B):
+            ws = torch.zeros(need, dtype=torch.uint8, device=self.device)
             self._ws[B] = ws
-        return ws
+            return ws
+        if self._scratch is None or self._scratch.numel() < need:
+            self._scratch = torch.zeros(need, dtype=torch.uint8, device=self.device)
+        return self._scratch
+
+    def _check_previous_call(self) -> None:
+        if self._err_flag[0] != 0:
+            self._err_flag[0] = 0
+            for ws in self._ws.values():  # launch counts restart from zero
+                ws.zero_()
+            raise N.ZmoeError(
+                "moe_layer: a wait for data exchanged between workgroups gave up in an earlier call "
+                "(another kernel occupying CUs of this GPU?); that call's outputs are NaN where affected")
 
     def __call__(self, x: torch.Tensor, *, return_routing: bool = False):
         if x.dtype != torch.bfloat16:
@@ -176,6 +224,7 @@ class QuantizedMoELayer:
         if return_routing:
             idx = torch.empty((B, self.top_k), dtype=torch.int32, device=self.device)
             w = torch.empty((B, self.top_k), dtype=torch.float32, device=self.device)
+        self._check_previous_call()
         ws = self._workspace(B)
         rc = N.lib().zmoe_moe_layer(
             torch.cuda.current_stream(self.device).cuda_stream, ctypes.byref(self.desc), xc.data_ptr(), B,
@@ -204,7 +253,8 @@ class QuantizedMoELayer:
         return ws[off: off + 8 * n].view(torch.int64).reshape(nb.value, ns.value).clone()
 
     def sync_error(self) -> int:
-        """Sticky error word of the fused kernel's cross-workgroup waits (0 = ok)."""
+        """Sticky error word of the single-launch kernels' cross-workgroup
+        waits, over every workspace (0 = ok).  Synchronises."""
         flags = 0
         for ws in self._ws.values():
             flags |= int(ws[128:132].view(torch.int32).item())
