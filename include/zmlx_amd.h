@@ -278,6 +278,21 @@ size_t zmoe_moe_layer_workspace_size(const zmoe_layer_desc* desc, int B);
 int zmoe_moe_layer(void* stream, const zmoe_layer_desc* desc, const void* x, int B, void* out,
                    uint32_t* out_idx, float* out_w, void* workspace, size_t workspace_bytes);
 
+/*
+ * zmoe_moe_layer without a workspace argument: allocates nothing (no
+ * hipMalloc / hipFree, no allocating library call), for callers that cannot
+ * allocate -- code under HIP graph capture, tight serving loops, harnesses
+ * that forbid it.  No counterpart in the reference.  It runs the kernel
+ * sequence with its buffers in a library-owned device array of
+ * zmoe_moe_layer_noalloc_max_bytes() bytes per GPU (held until the process
+ * ends); a batch whose buffers exceed it is rejected (ZMOE_EINVAL_SHAPE).
+ * Outputs equal zmoe_moe_layer's.  Calls that overlap on one GPU share the
+ * array and race: issue them on one stream.
+ */
+int zmoe_moe_layer_noalloc(void* stream, const zmoe_layer_desc* desc, const void* x, int B, void* out,
+                           uint32_t* out_idx, float* out_w);
+size_t zmoe_moe_layer_noalloc_max_bytes(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -128,6 +128,9 @@ _SIGNATURES = {
     "zmoe_moe_layer": (
         c_int, [c_void_p, ctypes.POINTER(LayerDesc), c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                 c_size_t]),
+    "zmoe_moe_layer_noalloc": (
+        c_int, [c_void_p, ctypes.POINTER(LayerDesc), c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
+    "zmoe_moe_layer_noalloc_max_bytes": (c_size_t, []),
 }
 
 _lock = threading.Lock()

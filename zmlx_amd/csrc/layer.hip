@@ -7,6 +7,7 @@
 #include "zmoe_host.h"
 
 #include <cstdlib>
+#include <mutex>
 #include <string>
 
 namespace zmoe {
@@ -185,6 +186,9 @@ extern "C" size_t zmoe_moe_layer_trace_info(const zmoe_layer_desc* desc, int B, 
   return fused_trace_info(desc, B, n_blocks, n_slots);
 }
 
+static int run_sequence(void* stream, const zmoe_layer_desc* d, const void* x, int B, void* out, uint32_t* out_idx,
+                        float* out_w, char* ws_base);
+
 extern "C" int zmoe_moe_layer(void* stream, const zmoe_layer_desc* d, const void* x, int B, void* out,
                               uint32_t* out_idx, float* out_w, void* workspace, size_t workspace_bytes) {
   int rc = validate_layer(d, B);
@@ -196,9 +200,19 @@ extern "C" int zmoe_moe_layer(void* stream, const zmoe_layer_desc* d, const void
   if (use_fused(d, B)) {
     return launch_fused(as_stream(stream), d, x, B, out, out_idx, out_w, workspace);
   }
+  ZMOE_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, ZMOE_EINVAL_SHAPE,
+               "[moe_layer] x must be 16-byte and workspace 256-byte aligned.");
   // multi-kernel sequence: its buffers follow the single-launch kernel's
-  LayerWs ws = layout_ws(d, B, static_cast<char*>(workspace) + multi_ws_offset(d, B));
-  ZMOE_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(workspace) & 255) == 0,
+  return run_sequence(stream, d, x, B, out, out_idx, out_w, static_cast<char*>(workspace) + multi_ws_offset(d, B));
+}
+
+// The multi-kernel sequence over workspace buffers at ws_base (layout_ws);
+// keeps nothing from call to call.
+static int run_sequence(void* stream, const zmoe_layer_desc* d, const void* x, int B, void* out, uint32_t* out_idx,
+                        float* out_w, char* ws_base) {
+  int rc = ZMOE_OK;
+  LayerWs ws = layout_ws(d, B, ws_base);
+  ZMOE_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(ws_base) & 255) == 0,
                ZMOE_EINVAL_SHAPE, "[moe_layer] x must be 16-byte and workspace 256-byte aligned.");
   hipStream_t st = as_stream(stream);
   const int H = d->hidden, E = d->n_experts, K = d->top_k, I = d->inter;
@@ -368,4 +382,57 @@ extern "C" int zmoe_moe_layer(void* stream, const zmoe_layer_desc* d, const void
     if (rc) return rc;
   }
   return ZMOE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// The layer without a caller workspace, for callers that cannot allocate
+// ---------------------------------------------------------------------------
+// The kernel sequence's buffers live in `scratch`, a file-scope device array
+// of kNoAllocScratchBytes that every GPU the library runs on holds until the
+// process ends.  Host code never passes `scratch` itself to a kernel: on the
+// host the name is a stand-in, not a device address.  The device address is
+// taken once per device with hipGetSymbolAddress, with that device current,
+// and kept in g_scratch_ptr.  The sequence keeps nothing from call to call
+// and writes every buffer before reading it, so nothing needs clearing; calls
+// that overlap on one GPU (two streams, or two host threads) share the array
+// and race.
+constexpr size_t kNoAllocScratchBytes = static_cast<size_t>(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static char* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+static int scratch_ptr(char** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  ZMOE_REQUIRE(e == hipSuccess, ZMOE_EHIP, std::string("[moe_layer_noalloc] hipGetDevice failed: ") + hipGetErrorString(e));
+  ZMOE_REQUIRE(dev >= 0 && dev < kMaxDevices, ZMOE_EUNSUPPORTED, "[moe_layer_noalloc] device index out of range.");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    ZMOE_REQUIRE(e == hipSuccess && p != nullptr, ZMOE_EHIP,
+                 std::string("[moe_layer_noalloc] hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<char*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return ZMOE_OK;
+}
+
+extern "C" size_t zmoe_moe_layer_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int zmoe_moe_layer_noalloc(void* stream, const zmoe_layer_desc* d, const void* x, int B, void* out,
+                                      uint32_t* out_idx, float* out_w) {
+  int rc = validate_layer(d, B);
+  if (rc) return rc;
+  if (B == 0) return ZMOE_OK;
+  const size_t need = layout_ws(d, B, nullptr).bytes;
+  ZMOE_REQUIRE(need <= kNoAllocScratchBytes, ZMOE_EINVAL_SHAPE,
+               "[moe_layer_noalloc] this batch needs " + std::to_string(need) + " bytes of scratch; the maximum is " +
+                   std::to_string(kNoAllocScratchBytes) + " (use zmoe_moe_layer with a workspace).");
+  char* base = nullptr;
+  rc = scratch_ptr(&base);
+  if (rc) return rc;
+  return run_sequence(stream, d, x, B, out, out_idx, out_w, base);
 }
