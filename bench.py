@@ -13,17 +13,22 @@ A step = one pass of the MoE block over the batch through all 48 layer copies
   value       us per token per layer call at B (lower is better)
   gbps        algorithmic HBM bytes per layer call / layer time
   roofline    of the dominant kernel -- the single-launch layer kernel
-              k_moe_decode1, one launch per layer call -- from HIP events on
-              the stream it runs on, around the timed region; `traffic` is the
-              measured HBM bytes per launch from the committed rocprofv3
-              counter summary (profiles/k_moe_decode1_qwen3_b1_traffic.json)
+              k_moe_decode1x (XCD-partitioned), one launch per layer call --
+              from HIP events on the stream it runs on, around the timed
+              region; `traffic` is the measured HBM bytes per launch from the
+              committed rocprofv3 counter summary
+              (profiles/k_moe_decode1x_qwen3_b1_counters.json)
   cpu_baseline  this repo's C++/OpenMP restatement of the unpatched MLX path
               (MLX is not installable offline) on the host cores, rank 0.
+  batches     B = 4 and 16 decode lines, the 512-token prefill line
+              (config 4) and, unless --no-other-configs, the LFM2, GLM-mxfp4
+              and DeepSeek-V3 lines (configs 0, 2, 4).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B]
-       python bench.py --all-configs          # + LFM2, GLM-mxfp4, DeepSeek-V3 lines
-       python bench.py --profile-run          # short run for rocprofv3 --pmc
-       python bench.py --summarize-pmc DIR     # FETCH_SIZE/WRITE_SIZE -> traffic
+       python bench.py --no-other-configs     # Qwen3 lines only
+       python bench.py --profile-run [--batch B]   # short run for rocprofv3 --pmc
+       python bench.py --summarize-pmc OUT FETCH_DIR WRITE_DIR [MFMA_DIR]
+       python bench.py --phase-trace          # per-phase stamps of the B=1 kernel
 """
 
 from __future__ import annotations
@@ -42,8 +47,11 @@ HBM_PEAK_GBPS = 8000.0
 H, E, K, I, GS = 2048, 128, 8, 768, 64
 LAYERS = 48
 ROOT = Path(__file__).resolve().parent
-TRAFFIC_FILE = ROOT / "profiles" / "k_moe_decode1_qwen3_b1_traffic.json"
 COPY_BYTES = 256 << 20  # calibration copy of --profile-run: reads and writes this many bytes
+# the single-launch kernel of each decode batch (rocprofv3 kernel names)
+DECODE_KERNELS = {1: "zmoe::k_moe_decode1x<0, 2, 768>"}
+# committed rocprofv3 counter summaries (profiles/<name>.json) of the decode lines
+COUNTER_FILES = {1: "k_moe_decode1x_qwen3_b1_counters"}
 
 
 def log(msg: str) -> None:
@@ -184,18 +192,7 @@ def prefill_line(layers, B, gen, dev, steps, warmup):
             "gbps": round(gbps, 1), "roofline_frac": round(gbps / HBM_PEAK_GBPS, 4),
             "tflops": round(flops / (layer_us * 1e-6) / 1e12, 2), "mfma_frac_bf16": round(flops / (layer_us * 1e-6) / 2.5e15, 4),
             "unique_experts": round(avg_unique, 2), "max_expert_rows": max(loads), "min_expert_rows": min(loads),
-            "alg_bytes_per_call": int(alg_bytes), "steps": steps}
-
-
-def load_traffic():
-    """HBM bytes per k_moe_decode launch measured by rocprofv3 (FETCH_SIZE and
-    WRITE_SIZE, calibrated on a copy kernel), if the summary is committed."""
-    try:
-        with open(TRAFFIC_FILE) as f:
-            t = json.load(f)
-        return t
-    except (OSError, ValueError):
-        return None
+            "alg_bytes_per_call": int(alg_bytes), "steps": steps, "counters": prefill_counters()}
 
 
 def profile_run(args) -> int:
@@ -213,43 +210,175 @@ def profile_run(args) -> int:
     layers, _ = build_layers(dev, args.layers)
     gen = torch.Generator(device=dev)
     gen.manual_seed(1234)
-    x = torch.randn((args.batch, H), generator=gen, device=dev).to(torch.bfloat16)
+    if args.batch >= 32:  # the prefill line's Zipf-skewed tokens
+        x = prefill_x(layers[0], args.batch, gen, dev)
+    else:
+        x = torch.randn((args.batch, H), generator=gen, device=dev).to(torch.bfloat16)
     ms = time_layers(layers, x, args.steps, args.warmup)
-    log(f"profile run: {ms * 1e3 / len(layers):.2f} us per layer call")
+    log(f"profile run: B={args.batch} {ms * 1e3 / len(layers):.2f} us per layer call")
     return 0
 
 
-def summarize_pmc(fetch_dir: str, write_dir: str) -> int:
-    """Turns two rocprofv3 --pmc runs of --profile-run (FETCH_SIZE, then
-    WRITE_SIZE; KiB per dispatch) into bytes per k_moe_decode launch, each
-    scaled by the factor that makes the calibration copy read/write exactly
-    COPY_BYTES."""
-    def per_kernel(d, counter):
-        vals = {}
-        for path in Path(d).rglob("*counter_collection.csv"):
-            with open(path) as f:
-                for row in csv.DictReader(f):
-                    if row.get("Counter_Name") != counter:
-                        continue
-                    vals.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
-        return vals
+def _pmc_rows(d: str):
+    """(kernel name, counter, value) rows of a rocprofv3 --pmc CSV run."""
+    for path in Path(d).rglob("*counter_collection.csv"):
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                yield row["Kernel_Name"], row.get("Counter_Name"), float(row["Counter_Value"])
 
-    out = {}
+
+def _short_kernel(name: str) -> str:
+    """Kernel name without its return type and parameter list (template
+    arguments kept)."""
+    name = name.replace("void ", "", 1)
+    depth = 0
+    for i, ch in enumerate(name):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            return name[:i]
+    return name
+
+
+def summarize_pmc(out_path: str, fetch_dir: str, write_dir: str, mfma_dir: str | None = None) -> int:
+    """Turns rocprofv3 --pmc runs of --profile-run into per-kernel HBM bytes
+    per dispatch: FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each scaled by
+    the factor that makes the run's calibration copy move exactly COPY_BYTES.
+    With a third run of SQ_VALU_MFMA_BUSY_CYCLES, GRBM_GUI_ACTIVE and
+    SQ_INSTS_VALU_MFMA_MOPS_BF16 it adds each kernel's MFMA utilisation
+    (rocprofv3's MfmaUtil: busy cycles summed over SIMDs / (GUI-active cycles
+    x SIMDs)) and the bf16 MFMA flops it executed (MOPS x 512)."""
+    out: dict = {"kernels": {}}
     for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
-        vals = per_kernel(d, counter)
+        vals: dict = {}
+        for k, c, v in _pmc_rows(d):
+            if c in (None, counter):
+                vals.setdefault(k, []).append(v)
         copy = [v for k, vs in vals.items() if "copy" in k.lower() or "elementwise" in k.lower() for v in vs]
-        dec = [v for k, vs in vals.items() if "k_moe_decode" in k for v in vs]
-        if not copy or not dec:
-            print(f"no copy / k_moe_decode dispatches for {counter} in {d}", file=sys.stderr)
+        if not copy:
+            print(f"no calibration copy for {counter} in {d}", file=sys.stderr)
             return 1
-        copy_kib = max(copy)
-        factor = (COPY_BYTES / 1024.0) / copy_kib
-        dec_kib = sum(dec) / len(dec)
-        out[counter] = {"copy_kib": copy_kib, "factor": factor, "k_moe_decode_kib_avg": dec_kib,
-                        "k_moe_decode_bytes": dec_kib * 1024.0 * factor, "dispatches": len(dec)}
-    out["bytes_per_launch"] = out["FETCH_SIZE"]["k_moe_decode_bytes"] + out["WRITE_SIZE"]["k_moe_decode_bytes"]
+        factor = (COPY_BYTES / 1024.0) / max(copy)
+        out[counter + "_calibration"] = {"copy_kib": max(copy), "factor": factor}
+        for k, vs in vals.items():
+            if not k.lstrip("void ").startswith("zmoe::"):
+                continue
+            rec = out["kernels"].setdefault(_short_kernel(k), {})
+            rec[counter.lower() + "_bytes"] = sum(vs) / len(vs) * 1024.0 * factor
+            rec["dispatches"] = len(vs)
+    for rec in out["kernels"].values():
+        rec["bytes"] = rec.get("fetch_size_bytes", 0.0) + rec.get("write_size_bytes", 0.0)
+    if mfma_dir:
+        simds = 4 * 256  # MI355X: 256 CUs x 4 SIMDs
+        acc: dict = {}
+        for k, c, v in _pmc_rows(mfma_dir):
+            if k.lstrip("void ").startswith("zmoe::"):
+                acc.setdefault(_short_kernel(k), {}).setdefault(c, []).append(v)
+        for k, cs in acc.items():
+            rec = out["kernels"].setdefault(k, {})
+            busy = sum(cs.get("SQ_VALU_MFMA_BUSY_CYCLES", [0])) / max(1, len(cs.get("SQ_VALU_MFMA_BUSY_CYCLES", [1])))
+            gui = sum(cs.get("GRBM_GUI_ACTIVE", [0])) / max(1, len(cs.get("GRBM_GUI_ACTIVE", [1])))
+            mops = sum(cs.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", [0])) / max(1, len(cs.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", [1])))
+            rec["mfma_busy_cycles"] = busy
+            rec["gui_active_cycles"] = gui
+            rec["mfma_util"] = busy / (gui * simds) if gui else None
+            rec["mfma_bf16_flops"] = mops * 512
+    with open(out_path, "w") as f:
+        json.dump(out, f, indent=1)
     print(json.dumps(out, indent=1))
     return 0
+
+
+# Phase stamps of the XCD-partitioned one-token kernel (k_moe_decode1x), by
+# trace slot: thread 0 of each workgroup, 100 MHz realtime counter.
+PHASES = [
+    (0, "kernel start (workgroup running)"),
+    (1, "R: router rows of this XCD computed and stored, x tile written"),
+    (3, "T: the XCD's logits polled from L2"),
+    (4, "T: softmax and ranking done"),
+    (5, "T: after the workgroup barrier (unit known)"),
+    (13, "A: gate/up loads issued"),
+    (6, "A: gate/up rows computed"),
+    (7, "A: down-projection loads issued, act words stored"),
+    (8, "D: act row staged in LDS from L2"),
+    (9, "D: after the workgroup barrier"),
+    (11, "D: down rows computed"),
+    (10, "D: unit outputs stored (device scope)"),
+    (12, "C: combine done (combining workgroups) / exit"),
+]
+
+
+def phase_trace(args) -> int:
+    """Per-phase timing of the B=1 layer kernel: the untraced per-call time,
+    then one traced graph replay whose stamps give, per phase, the median
+    over workgroups and the latest workgroup (median over the 48 layer
+    calls), relative to the earliest workgroup start of each call."""
+    import statistics as st
+
+    import torch
+
+    from zmlx_amd import _native as N
+
+    dev = torch.device("cuda:0")
+    layers, _ = build_layers(dev, args.layers)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+    x = torch.randn((1, H), generator=gen, device=dev).to(torch.bfloat16)
+    ms = time_layers(layers, x, args.steps, args.warmup)
+    print(f"untraced: {ms * 1e3 / len(layers):.2f} us per layer call")
+    for layer in layers:
+        layer.desc.flags |= N.LAYER_TRACE
+    ms_t = time_layers(layers, x, args.steps, args.warmup)
+    print(f"traced:   {ms_t * 1e3 / len(layers):.2f} us per layer call")
+    med: dict = {}
+    last: dict = {}
+    ends = []
+    for layer in layers:
+        t = layer.phase_trace(1).cpu()
+        t0 = int(t[:, 0].min())
+        ends.append((int(t.max()) - t0) * 0.01)
+        for slot, _ in PHASES:
+            col = [(int(v) - t0) * 0.01 for v in t[:, slot].tolist() if int(v) >= t0]
+            if col:
+                med.setdefault(slot, []).append(st.median(col))
+                last.setdefault(slot, []).append(max(col))
+    print("| slot | phase | median workgroup (us) | latest workgroup (us) |")
+    print("|---|---|---|---|")
+    for slot, name in PHASES:
+        if slot in med:
+            print(f"| {slot} | {name} | {st.median(med[slot]):.2f} | {st.median(last[slot]):.2f} |")
+    print(f"| | last workgroup done | | {st.median(ends):.2f} |")
+    errs = sum(layer.sync_error() for layer in layers)
+    print(f"sticky error words: {errs}")
+    return 0
+
+
+def prefill_counters():
+    """Per-kernel HBM bytes and MFMA activity of the prefill line's grouped
+    GEMMs from the committed rocprofv3 counter summary
+    (profiles/k_grouped_qmm_qwen3_prefill512_counters.json), or None."""
+    prof = load_profile("k_grouped_qmm_qwen3_prefill512_counters")
+    if not prof:
+        return None
+    out = {}
+    for k, rec in prof.get("kernels", {}).items():
+        if "k_grouped_qmm" not in k:
+            continue
+        out[k] = {"hbm_bytes": int(rec["bytes"]) if "bytes" in rec else None,
+                  "mfma_util": round(rec["mfma_util"], 4) if rec.get("mfma_util") is not None else None,
+                  "mfma_bf16_flops": rec.get("mfma_bf16_flops")}
+    return out
+
+
+def load_profile(name: str):
+    """A committed counter summary (profiles/<name>.json), or None."""
+    try:
+        with open(ROOT / "profiles" / f"{name}.json") as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
 
 
 def cpu_baseline(base, layer0, x_host, budget_s: float = 12.0, max_tokens: int = 4096):
@@ -280,13 +409,16 @@ def cpu_baseline(base, layer0, x_host, budget_s: float = 12.0, max_tokens: int =
         ref_lib.moe_layer_qwen_bits(x16[n % x16.shape[0]:][:1], wr, banks["gate"], banks["up"], banks["down"], k=K)
         n += 1
     dt = time.perf_counter() - t0
+    alg = K * per_expert_bytes() + E * H * 2 + 4 * H
     return {
         "value": round(dt * 1e6 / n, 2),
         "unit": "us/token",
+        "gbps": round(alg * n / dt / 1e9, 2),
         "cores": threads,
         "kind": "port",
         "sample": f"{n} single-token calls of one Qwen3-shaped layer copy (B=1), "
-                  f"C++/OpenMP restatement of the unpatched MLX path (MLX unavailable offline), {dt:.1f}s",
+                  f"C++/OpenMP restatement of the unpatched MLX path (MLX unavailable offline; AVX2, one "
+                  f"parallel region per token), {dt:.1f}s",
     }
 
 
@@ -381,15 +513,19 @@ def main() -> int:
     ap.add_argument("--extra-batches", default="4,16")
     ap.add_argument("--prefill", type=int, default=512,
                     help="tokens of the prefill line (config 4; 0 skips it)")
-    ap.add_argument("--all-configs", action="store_true",
-                    help="also measure the other BASELINE configs (LFM2, GLM-mxfp4, DeepSeek-V3)")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the other BASELINE configs (LFM2, GLM-mxfp4, DeepSeek-V3)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     ap.add_argument("--profile-run", action="store_true", help="short run for rocprofv3 counter passes")
-    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
+    ap.add_argument("--phase-trace", action="store_true", help="per-phase stamps of the B=1 layer kernel")
+    ap.add_argument("--summarize-pmc", nargs="+", metavar="PATH",
+                    help="OUT_JSON FETCH_DIR WRITE_DIR [MFMA_DIR]: per-kernel counter summary")
     args = ap.parse_args()
     if args.summarize_pmc:
+        if len(args.summarize_pmc) not in (3, 4):
+            ap.error("--summarize-pmc OUT_JSON FETCH_DIR WRITE_DIR [MFMA_DIR]")
         return summarize_pmc(*args.summarize_pmc)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -404,6 +540,8 @@ def main() -> int:
 
     if args.profile_run:
         return profile_run(args)
+    if args.phase_trace:
+        return phase_trace(args)
     dev = torch.device("cuda:0")
     log(f"building {args.layers} layer copies (this takes a few seconds)")
     layers, base = build_layers(dev, args.layers)
@@ -434,12 +572,12 @@ def main() -> int:
             main_rec = rec
             # one k_moe_decode launch per layer call: the timed region holds
             # steps x layers launches and nothing else
-            tr = load_traffic() if B == 1 else None
+            kname = DECODE_KERNELS.get(B, "zmoe::k_moe_decodeb<0, 2, 4>")
+            tr = (load_profile(COUNTER_FILES.get(B, "")) or {}).get("kernels", {}).get(kname)
             roof = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                     "frac": round(gbps / HBM_PEAK_GBPS, 4),
-                    "traffic": int(tr["bytes_per_launch"]) if tr else None,
-                    "kernel": "k_moe_decode1 (one-token single-launch MoE layer)" if B == 1 else
-                              "k_moe_decodeb (batched single-launch MoE layer)",
+                    "traffic": int(tr["bytes"]) if tr else None,
+                    "kernel": kname,
                     "avg_launch_us": round(layer_us, 3),
                     "alg_bytes_per_launch": int(alg_bytes)}
         log(f"B={B}: {rec}")
@@ -448,7 +586,8 @@ def main() -> int:
         per_b["prefill"] = prefill_line(layers, args.prefill, gen, dev, max(3, args.steps // 10), args.warmup)
         log(f"prefill: {per_b['prefill']}")
 
-    if args.all_configs:
+    n_copies = len(layers)
+    if not args.no_other_configs:
         layers = layers[:1]  # the CPU baseline reads the first copy
         torch.cuda.empty_cache()
         per_b["configs"] = other_config_lines(dev, max(5, args.steps // 5), args.warmup)
@@ -474,7 +613,7 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "qwen3-30b-a3b-moe-layer-decode", "hidden": H, "experts": E, "top_k": K,
-                   "inter": I, "quant": "affine4-g64", "batch": args.batch, "layer_copies": len(layers),
+                   "inter": I, "quant": "affine4-g64", "batch": args.batch, "layer_copies": n_copies,
                    "parallelism": "none (1 GPU)"},
         "gbps": main_rec["gbps"],
         "roofline": roof,

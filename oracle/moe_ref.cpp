@@ -10,9 +10,17 @@
 //   SwiGLU             nn.silu(g) * u  (tests/test_gather_qmm_swiglu.py:73)
 //   Qwen gating        patch/patterns/moe_mlp.py:255-266
 //   native combine     (y * w[..., None]).sum(-2)   moe_mlp.py:1043
-// Accumulation here is fp32 per group (s*sum(q*x) + b*sum(x), the factoring
-// MLX's qmv kernels use), so results agree with the float64 oracle to within
-// fp32 rounding, not bit for bit.
+// Accumulation is fp32 per group (s*sum(q*x) + b*sum(x), the factoring MLX's
+// qmv kernels use), so results agree with the float64 oracle to within fp32
+// rounding, not bit for bit.
+//
+// Built for x86-64-v3 (AVX2 + FMA): the nibbles of one packed word are
+// unpacked into 8 int32 lanes with one variable shift and a mask, converted
+// and multiplied into 8 activations with one FMA.  One OpenMP parallel region
+// per token covers the router, the gate/up rows of all selected experts, the
+// down rows and the combine (barriers between them), so the threads stay in
+// one team for the whole token.
+#include <immintrin.h>
 #include <omp.h>
 #include <stdint.h>
 
@@ -40,25 +48,64 @@ inline uint16_t to_bf(float f) {
 
 inline float rbf(float f) { return bf(to_bf(f)); }
 
-// y[n] = bf16( sum_g s[n,g]*sum(q*x) + b[n,g]*sum(x) ) for rows n of one
-// affine 4-bit matrix [N, K/8].
-void qmv_affine(const uint32_t* w, const uint16_t* s, const uint16_t* b, const float* x, int N, int K, int gs,
-                uint16_t* y) {
-  const int G = K / gs;
-#pragma omp parallel for schedule(static)
-  for (int n = 0; n < N; ++n) {
-    const uint32_t* wr = w + static_cast<int64_t>(n) * (K / 8);
-    float acc = 0.0f;
-    for (int g = 0; g < G; ++g) {
-      float qx = 0.0f, sx = 0.0f;
-      for (int i = g * gs; i < (g + 1) * gs; ++i) {
-        const float q = static_cast<float>((wr[i >> 3] >> ((i & 7) * 4)) & 0xFu);
-        qx += q * x[i];
-        sx += x[i];
-      }
-      acc += bf(s[static_cast<int64_t>(n) * G + g]) * qx + bf(b[static_cast<int64_t>(n) * G + g]) * sx;
+inline float hsum8(__m256 v) {
+  __m128 lo = _mm256_castps256_ps128(v), hi = _mm256_extractf128_ps(v, 1);
+  lo = _mm_add_ps(lo, hi);
+  lo = _mm_add_ps(lo, _mm_movehl_ps(lo, lo));
+  lo = _mm_add_ss(lo, _mm_movehdup_ps(lo));
+  return _mm_cvtss_f32(lo);
+}
+
+// One row of an affine 4-bit matrix against fp32 activations x[K] whose
+// per-group sums are xg[K/gs]:  bf16( sum_g s_g * sum(q*x) + b_g * sum(x) ).
+inline uint16_t qrow_affine(const uint32_t* w, const uint16_t* s, const uint16_t* b, const float* x, const float* xg,
+                            int K, int gs) {
+  const __m256i shifts = _mm256_setr_epi32(0, 4, 8, 12, 16, 20, 24, 28);
+  const __m256i mask = _mm256_set1_epi32(0xF);
+  const int G = K / gs, wpg = gs / 8;
+  float acc = 0.0f;
+  for (int g = 0; g < G; ++g) {
+    __m256 a0 = _mm256_setzero_ps(), a1 = _mm256_setzero_ps();
+    const uint32_t* wg = w + g * wpg;
+    const float* xp = x + g * gs;
+    int j = 0;
+    for (; j + 1 < wpg; j += 2) {
+      const __m256i q0 = _mm256_and_si256(_mm256_srlv_epi32(_mm256_set1_epi32(static_cast<int>(wg[j])), shifts), mask);
+      const __m256i q1 = _mm256_and_si256(_mm256_srlv_epi32(_mm256_set1_epi32(static_cast<int>(wg[j + 1])), shifts), mask);
+      a0 = _mm256_fmadd_ps(_mm256_cvtepi32_ps(q0), _mm256_loadu_ps(xp + 8 * j), a0);
+      a1 = _mm256_fmadd_ps(_mm256_cvtepi32_ps(q1), _mm256_loadu_ps(xp + 8 * j + 8), a1);
     }
-    y[n] = to_bf(acc);
+    for (; j < wpg; ++j) {
+      const __m256i q0 = _mm256_and_si256(_mm256_srlv_epi32(_mm256_set1_epi32(static_cast<int>(wg[j])), shifts), mask);
+      a0 = _mm256_fmadd_ps(_mm256_cvtepi32_ps(q0), _mm256_loadu_ps(xp + 8 * j), a0);
+    }
+    const float qx = hsum8(_mm256_add_ps(a0, a1));
+    acc += bf(s[g]) * qx + bf(b[g]) * xg[g];
+  }
+  return to_bf(acc);
+}
+
+// Dot of fp32 x[H] with one bf16 row.
+inline float dot_bf16(const float* x, const uint16_t* r, int H) {
+  __m256 a0 = _mm256_setzero_ps(), a1 = _mm256_setzero_ps();
+  int h = 0;
+  for (; h + 16 <= H; h += 16) {
+    const __m256i v0 = _mm256_slli_epi32(_mm256_cvtepu16_epi32(_mm_loadu_si128(reinterpret_cast<const __m128i*>(r + h))), 16);
+    const __m256i v1 =
+        _mm256_slli_epi32(_mm256_cvtepu16_epi32(_mm_loadu_si128(reinterpret_cast<const __m128i*>(r + h + 8))), 16);
+    a0 = _mm256_fmadd_ps(_mm256_castsi256_ps(v0), _mm256_loadu_ps(x + h), a0);
+    a1 = _mm256_fmadd_ps(_mm256_castsi256_ps(v1), _mm256_loadu_ps(x + h + 8), a1);
+  }
+  float acc = hsum8(_mm256_add_ps(a0, a1));
+  for (; h < H; ++h) acc += x[h] * bf(r[h]);
+  return acc;
+}
+
+void group_sums(const float* x, int K, int gs, float* xg) {
+  for (int g = 0; g < K / gs; ++g) {
+    float s = 0.0f;
+    for (int i = g * gs; i < (g + 1) * gs; ++i) s += x[i];
+    xg[g] = s;
   }
 }
 
@@ -80,49 +127,66 @@ void oref_moe_layer_qwen(const uint16_t* x, int B, int H, int E, int K, int I, i
                          const uint16_t* wr, const uint32_t* gw, const uint16_t* gsc, const uint16_t* gb,
                          const uint32_t* uw, const uint16_t* usc, const uint16_t* ub, const uint32_t* dw,
                          const uint16_t* dsc, const uint16_t* db, uint16_t* out, int32_t* out_idx) {
-  std::vector<float> xf(H), logit(E), act_f(I);
-  std::vector<uint16_t> g(I), u(I), act(I), y(static_cast<size_t>(K) * H);
+  std::vector<float> xf(H), xg(H / gs), logit(E), p(E), act(static_cast<size_t>(K) * I), ag(static_cast<size_t>(K) * (I / gs)),
+      wk(K);
+  std::vector<uint16_t> y(static_cast<size_t>(K) * H);
+  std::vector<int> sel(K);
   const int64_t gsz = static_cast<int64_t>(I) * (H / 8), gss = static_cast<int64_t>(I) * (H / gs);
   const int64_t dsz = static_cast<int64_t>(H) * (I / 8), dss = static_cast<int64_t>(H) * (I / gs);
   for (int t = 0; t < B; ++t) {
     for (int h = 0; h < H; ++h) xf[h] = bf(x[static_cast<int64_t>(t) * H + h]);
-#pragma omp parallel for schedule(static)
-    for (int e = 0; e < E; ++e) {
-      float acc = 0.0f;
-      for (int h = 0; h < H; ++h) acc += xf[h] * bf(wr[static_cast<int64_t>(e) * H + h]);
-      logit[e] = rbf(acc);
-    }
-    float m = -INFINITY;
-    for (int e = 0; e < E; ++e) m = std::max(m, logit[e]);
-    float sum = 0.0f;
-    std::vector<float> p(E);
-    for (int e = 0; e < E; ++e) sum += (p[e] = std::exp(logit[e] - m));
-    for (int e = 0; e < E; ++e) p[e] = rbf(p[e] / sum);
-    std::vector<int> order(E);
-    for (int e = 0; e < E; ++e) order[e] = e;
-    std::stable_sort(order.begin(), order.end(), [&](int a, int c) { return p[a] > p[c]; });
-    float tot = 0.0f;
-    for (int k = 0; k < K; ++k) tot += p[order[k]];
-    const float sb = rbf(tot);
-    for (int k = 0; k < K; ++k) {
-      const int e = order[k];
-      if (out_idx) out_idx[static_cast<int64_t>(t) * K + k] = e;
-      qmv_affine(gw + e * gsz, gsc + e * gss, gb + e * gss, xf.data(), I, H, gs, g.data());
-      qmv_affine(uw + e * gsz, usc + e * gss, ub + e * gss, xf.data(), I, H, gs, u.data());
-      for (int i = 0; i < I; ++i) {
-        const float gv = bf(g[i]);
+#pragma omp parallel
+    {
+#pragma omp for schedule(static)
+      for (int e = 0; e < E; ++e) logit[e] = rbf(dot_bf16(xf.data(), wr + static_cast<int64_t>(e) * H, H));
+#pragma omp single
+      {
+        group_sums(xf.data(), H, gs, xg.data());
+        float m = -INFINITY;
+        for (int e = 0; e < E; ++e) m = std::max(m, logit[e]);
+        float sum = 0.0f;
+        for (int e = 0; e < E; ++e) sum += (p[e] = std::exp(logit[e] - m));
+        for (int e = 0; e < E; ++e) p[e] = rbf(p[e] / sum);
+        std::vector<int> order(E);
+        for (int e = 0; e < E; ++e) order[e] = e;
+        std::stable_sort(order.begin(), order.end(), [&](int a, int c) { return p[a] > p[c]; });
+        float tot = 0.0f;
+        for (int k = 0; k < K; ++k) tot += p[order[k]];
+        const float sb = rbf(tot);
+        for (int k = 0; k < K; ++k) {
+          sel[k] = order[k];
+          wk[k] = norm ? rbf(p[order[k]] / sb) : p[order[k]];
+          if (out_idx) out_idx[static_cast<int64_t>(t) * K + k] = order[k];
+        }
+      }
+      // gate/up + SwiGLU rows of every selected expert
+#pragma omp for schedule(static)
+      for (int it = 0; it < K * I; ++it) {
+        const int k = it / I, n = it - k * I, e = sel[k];
+        const float gv = bf(qrow_affine(gw + e * gsz + static_cast<int64_t>(n) * (H / 8), gsc + e * gss + static_cast<int64_t>(n) * (H / gs),
+                                        gb + e * gss + static_cast<int64_t>(n) * (H / gs), xf.data(), xg.data(), H, gs));
+        const float u = bf(qrow_affine(uw + e * gsz + static_cast<int64_t>(n) * (H / 8), usc + e * gss + static_cast<int64_t>(n) * (H / gs),
+                                       ub + e * gss + static_cast<int64_t>(n) * (H / gs), xf.data(), xg.data(), H, gs));
         const float sig = rbf(1.0f / (1.0f + std::exp(-gv)));
-        act_f[i] = bf(to_bf(rbf(gv * sig) * bf(u[i])));
+        act[it] = bf(to_bf(rbf(gv * sig) * u));
       }
-      qmv_affine(dw + e * dsz, dsc + e * dss, db + e * dss, act_f.data(), H, I, gs, y.data() + static_cast<int64_t>(k) * H);
-    }
-    for (int h = 0; h < H; ++h) {
-      float acc = 0.0f;
-      for (int k = 0; k < K; ++k) {
-        const float wk = norm ? rbf(p[order[k]] / sb) : p[order[k]];
-        acc += rbf(wk * bf(y[static_cast<int64_t>(k) * H + h]));
+#pragma omp for schedule(static)
+      for (int k = 0; k < K; ++k) group_sums(act.data() + static_cast<size_t>(k) * I, I, gs, ag.data() + static_cast<size_t>(k) * (I / gs));
+      // down rows of every selected expert
+#pragma omp for schedule(static)
+      for (int it = 0; it < K * H; ++it) {
+        const int k = it / H, h = it - k * H, e = sel[k];
+        y[it] = qrow_affine(dw + e * dsz + static_cast<int64_t>(h) * (I / 8), dsc + e * dss + static_cast<int64_t>(h) * (I / gs),
+                            db + e * dss + static_cast<int64_t>(h) * (I / gs), act.data() + static_cast<size_t>(k) * I,
+                            ag.data() + static_cast<size_t>(k) * (I / gs), I, gs);
       }
-      out[static_cast<int64_t>(t) * H + h] = to_bf(acc);
+      // native combine, k ascending
+#pragma omp for schedule(static)
+      for (int h = 0; h < H; ++h) {
+        float acc = 0.0f;
+        for (int k = 0; k < K; ++k) acc += rbf(wk[k] * bf(y[static_cast<int64_t>(k) * H + h]));
+        out[static_cast<int64_t>(t) * H + h] = to_bf(acc);
+      }
     }
   }
 }

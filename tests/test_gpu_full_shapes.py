@@ -3,6 +3,7 @@
 - Qwen3-30B-A3B: hidden 2048, 128 experts, top-8 softmax router with
   renormalised weights, expert intermediate 768, affine 4-bit group 64;
   decode batches 1, 4 and 16 (the bench's workload);
+- Qwen3-30B-A3B prefill: 512 Zipf-skewed tokens (config 4);
 - DeepSeek-V3: hidden 7168, 256 routed experts in 8 groups (top-4 groups,
   top-8 experts, sigmoid + correction bias, routed scaling 2.5), one shared
   expert, expert intermediate 2048; decode batches 1 and 64 (the second runs
@@ -147,6 +148,57 @@ def test_qwen3_30b_a3b_full_shape(qwen3_layer, dev, B, checked):
     _, w_ref, _ = O.qwen_gating(logits, QK, True, idx=idx)
     assert O.bf16_ulp_diff(w, w_ref).max() <= 1
     rows = np.arange(checked)
+    experts = np.unique(idx[rows])
+    remap = np.searchsorted(experts, idx[rows])
+    banks = {n: _host_bank(*mats[n], experts) for n in ("gate", "up", "down")}
+    y = O.moe_experts(x[rows], remap, banks["gate"].as_tuple(), banks["up"].as_tuple(), banks["down"].as_tuple())
+    ref = O.bf16_round(O.moe_combine(y, O.bf16_round(w[rows]), "native"))
+    got = out[rows]
+    np.testing.assert_allclose(got, ref, atol=1e-2, rtol=1e-2)
+    ulp = O.bf16_ulp_diff(got, ref)
+    assert (ulp == 0).mean() >= 0.90, f"exact fraction {(ulp == 0).mean():.4f}"
+    assert np.isfinite(out).all()
+
+
+def _zipf_tokens(rng, wr, B, skew=1.1, peak=3.0):
+    """B tokens of N(0,1) plus a shared component along the router rows that
+    adds a Zipf-skewed logit offset peak * rank^-skew to the experts (ranks
+    over a random permutation): imbalanced expert loads, as the bench's
+    prefill line (config 4)."""
+    w = wr.astype(np.float64)
+    rank = np.empty(w.shape[0])
+    rank[rng.permutation(w.shape[0])] = np.arange(1, w.shape[0] + 1)
+    off = peak * rank ** -skew
+    v = ((off / (w * w).sum(1))[:, None] * w).sum(0)
+    return O.bf16_round(rng.standard_normal((B, w.shape[1])) + v[None, :]).astype(np.float32)
+
+
+def test_qwen3_prefill_512_zipf(qwen3_layer, dev):
+    """Config 4: 512 Zipf-skewed tokens over all 128 experts through the
+    layer's prefill path (pairs sorted by expert, grouped GEMMs on MFMA in
+    64-row chunks).  Every token's routing is checked against the full
+    router; the outputs of tokens that route to the heaviest expert -- the
+    first and last of its rows (its first and last chunk) -- and of two
+    others, through their experts read back, against the oracle."""
+    import torch
+
+    layer, mats, wr, _ = qwen3_layer
+    rng = np.random.default_rng(512)
+    B = 512
+    x = _zipf_tokens(rng, wr, B)
+    print("qwen3 prefill 512 zipf", flush=True)
+    out, idx, w = layer(to_bf16(x, dev), return_routing=True)
+    torch.cuda.synchronize()
+    idx, w, out = from_dev(idx).astype(np.int64), from_dev(w), from_dev(out)
+    logits = O.dense_logits(x, wr)
+    assert O.topk_is_valid(idx, O.softmax_precise_bf16(logits), QK).all()
+    _, w_ref, _ = O.qwen_gating(logits, QK, True, idx=idx)
+    assert O.bf16_ulp_diff(w, w_ref).max() <= 1
+    loads = np.bincount(idx.reshape(-1), minlength=QE)
+    heavy = int(loads.argmax())
+    assert loads[heavy] > 3 * 64, f"heaviest expert has only {loads[heavy]} rows (want 4+ chunks of 64)"
+    on_heavy = np.nonzero((idx == heavy).any(1))[0]
+    rows = np.unique(np.array([on_heavy[0], on_heavy[-1], 1, B // 2]))
     experts = np.unique(idx[rows])
     remap = np.searchsorted(experts, idx[rows])
     banks = {n: _host_bank(*mats[n], experts) for n in ("gate", "up", "down")}
