@@ -310,6 +310,7 @@ PHASES = [
 ]
 
 
+
 def phase_trace(args) -> int:
     """Per-phase timing of the B=1 layer kernel: the untraced per-call time,
     then one traced graph replay whose stamps give, per phase, the median
@@ -325,9 +326,14 @@ def phase_trace(args) -> int:
     layers, _ = build_layers(dev, args.layers)
     gen = torch.Generator(device=dev)
     gen.manual_seed(1234)
-    x = torch.randn((1, H), generator=gen, device=dev).to(torch.bfloat16)
+    B = args.batch
+    if B != 1:
+        print("--phase-trace: B=1 (the XCD-partitioned one-token kernel) only", file=sys.stderr)
+        return 2
+    x = torch.randn((B, H), generator=gen, device=dev).to(torch.bfloat16)
+    phases = PHASES
     ms = time_layers(layers, x, args.steps, args.warmup)
-    print(f"untraced: {ms * 1e3 / len(layers):.2f} us per layer call")
+    print(f"B={B} untraced: {ms * 1e3 / len(layers):.2f} us per layer call")
     for layer in layers:
         layer.desc.flags |= N.LAYER_TRACE
     ms_t = time_layers(layers, x, args.steps, args.warmup)
@@ -336,17 +342,17 @@ def phase_trace(args) -> int:
     last: dict = {}
     ends = []
     for layer in layers:
-        t = layer.phase_trace(1).cpu()
+        t = layer.phase_trace(B).cpu()
         t0 = int(t[:, 0].min())
         ends.append((int(t.max()) - t0) * 0.01)
-        for slot, _ in PHASES:
+        for slot, _ in phases:
             col = [(int(v) - t0) * 0.01 for v in t[:, slot].tolist() if int(v) >= t0]
             if col:
                 med.setdefault(slot, []).append(st.median(col))
                 last.setdefault(slot, []).append(max(col))
     print("| slot | phase | median workgroup (us) | latest workgroup (us) |")
     print("|---|---|---|---|")
-    for slot, name in PHASES:
+    for slot, name in phases:
         if slot in med:
             print(f"| {slot} | {name} | {st.median(med[slot]):.2f} | {st.median(last[slot]):.2f} |")
     print(f"| | last workgroup done | | {st.median(ends):.2f} |")

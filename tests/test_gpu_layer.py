@@ -248,6 +248,10 @@ def _layer_pair(dev, rng, family, *, H, E, I, K, mode="affine", gs=64, shared_I=
 
 FUSED_CASES = [
     ("qwen3", dict(H=2048, E=128, I=768, K=8), [1, 2, 4, 8, 16, 5]),
+    # one-token kernel with units other than 8; shared expert with batches
+    # (k_moe_decodeb)
+    ("qwen3_k6", dict(H=2048, E=64, I=768, K=6), [1, 3, 16]),
+    ("qwen3_shared", dict(H=2048, E=64, I=768, K=8, shared_I=768), [1, 2, 4, 3]),
     ("lfm2", dict(H=2048, E=32, I=1792, K=4), [1, 3, 16]),
     ("glm", dict(H=2048, E=64, I=1536, K=4, mode="mxfp4", gs=32, shared_I=1536), [1, 8, 16, 2]),
     ("deepseek", dict(H=1024, E=256, I=512, K=8, shared_I=512), [1, 2]),
@@ -336,7 +340,7 @@ def test_layer_expert_major_gemv(dev, mode, gs):
 @pytest.mark.parametrize("family,shape,B", [
     ("qwen3", dict(H=2048, E=32, I=768, K=8), 1),     # XCD-partitioned one-token kernel
     ("lfm2", dict(H=2048, E=32, I=1792, K=4), 1),     # one-token kernel
-    ("qwen3", dict(H=2048, E=32, I=768, K=8), 4),     # batched kernel
+    ("qwen3", dict(H=2048, E=32, I=768, K=8, shared_I=768), 4),  # batched kernel (shared expert)
 ])
 def test_wait_give_up_is_loud(dev, family, shape, B):
     """A single-launch kernel whose cross-workgroup wait gives up (forced from
@@ -352,7 +356,7 @@ def test_wait_give_up_is_loud(dev, family, shape, B):
 
     rng = np.random.default_rng(31)
     banks, wr, sh, tq, tsh, wr_t = _build(dev, rng, **shape)
-    layer = QuantizedMoELayer.for_family(family, wr_t, tq["gate"], tq["up"], tq["down"], top_k=shape["K"])
+    layer = QuantizedMoELayer.for_family(family, wr_t, tq["gate"], tq["up"], tq["down"], top_k=shape["K"], shared=tsh)
     assert layer._single_launch(B)
     x = to_bf16(bf16_randn(rng, (B, shape["H"])), dev)
     print(f"[give-up] {family} B={B}", flush=True)

@@ -505,9 +505,21 @@ size_t fused_lds_bytes(const zmoe_layer_desc* d, int B) {
   return ((sizeof(FusedLds) + 15) & ~static_cast<size_t>(15)) + (front > back ? front : back);
 }
 
+// Which batches take a single-launch kernel.  One token always (the kernel
+// sequence's launches dominate: Qwen3 13.0 vs 22.7 us, LFM2 19.2 vs 23.8,
+// GLM 19.1 vs 34.6, DeepSeek-V3 76.4 vs 82.9).  From two tokens on the
+// kernel sequence streams the experts at a higher rate than the batched
+// single-launch kernel gains on launches (Qwen3 B=2/4/8: 26.3/34.4/47.5 us
+// vs 30.5/43.0/63.5; LFM2 B=2: 29.7 vs 43.2), except for layers with a
+// shared expert, whose own kernels the sequence adds (GLM B=2/4: 31.5/46.3
+// vs 42.2/54.1 us; even at B=8) -- so batches of 2..kFusedSharedMaxB tokens
+// take k_moe_decodeb there.  (1 MI355X, 48 or 8 rotated layer copies.)
+constexpr int kFusedSharedMaxB = 4;
+
 bool fused_supported(const zmoe_layer_desc* d, int B) {
   if (num_cus() > kMaxGrid) return false;
-  if (B >= 2 && decodeb_supported(d, B, num_cus())) return true;
+  if (B >= 2)
+    return B <= kFusedSharedMaxB && d->shared_inter > 0 && decodeb_supported(d, B, num_cus());
   if (B < 1 || B > kFMaxB) return false;
   if (num_cus() > kMaxGrid) return false;
   if (d->hidden % 512 != 0 || d->hidden / 512 > kMaxNC) return false;
@@ -538,9 +550,10 @@ static size_t off_xy(const zmoe_layer_desc* d, int B) {
   return align256(off_trace(d, B) + static_cast<size_t>(num_cus()) * kTraceSlots * 8);
 }
 
-size_t fused_workspace_bytes(const zmoe_layer_desc* d, int B) {
-  return off_xy(d, B) + (B == 1 ? xcd_xy_bytes(d) : 0);
-}
+// tagged expert outputs of the XCD-partitioned one-token kernel
+static size_t xy_bytes(const zmoe_layer_desc* d, int B) { return B == 1 ? xcd_xy_bytes(d) : 0; }
+
+size_t fused_workspace_bytes(const zmoe_layer_desc* d, int B) { return off_xy(d, B) + xy_bytes(d, B); }
 
 size_t fused_trace_info(const zmoe_layer_desc* d, int B, int* n_blocks, int* n_slots) {
   *n_blocks = num_cus();
@@ -622,7 +635,7 @@ int launch_fused(hipStream_t st, const zmoe_layer_desc* d, const void* x, int B,
   fp.trace = (d->flags & ZMOE_LAYER_TRACE) ? reinterpret_cast<unsigned long long*>(base + off_trace(d, B)) : nullptr;
   fp.err_host = d->error_flag_host;
   fp.spin = d->spin_limit > 0 ? static_cast<unsigned>(d->spin_limit) : kSpinLimit;
-  fp.xy = B == 1 ? reinterpret_cast<uint32_t*>(base + off_xy(d, B)) : nullptr;
+  fp.xy = xy_bytes(d, B) > 0 ? reinterpret_cast<uint32_t*>(base + off_xy(d, B)) : nullptr;
   fp.by_S4H = make_fastdiv(static_cast<uint32_t>(d->hidden / 8));
   fp.by_SH = make_fastdiv(static_cast<uint32_t>(d->hidden / 32));
   fp.by_S4I = make_fastdiv(static_cast<uint32_t>(d->inter / 8));

@@ -312,6 +312,41 @@ __device__ __forceinline__ void seg_param_decode(RawParam r, float& s, float& c)
   }
 }
 
+// Dequantised bf16 pairs of one 16-byte weight segment, in the order
+// seg_dot consumes them (word x: pairs of nibbles (0,4) (1,5) (2,6) (3,7)).
+template <int QMODE>
+__device__ __forceinline__ void seg_dequant(const uint4 w, uint32_t (&d)[16], AffineK k) {
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (QMODE == ZMOE_Q_AFFINE) {
+      d[4 * i + 0] = (ws[i] & k.m) | k.o;
+      d[4 * i + 1] = ((ws[i] >> 4) & k.m) | k.o;
+      d[4 * i + 2] = ((ws[i] >> 8) & k.m) | k.o;
+      d[4 * i + 3] = ((ws[i] >> 12) & k.m) | k.o;
+    } else {
+      d[4 * i + 0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(ws[i], 1.0f, 0));
+      d[4 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(ws[i], 1.0f, 1));
+      d[4 * i + 2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(ws[i], 1.0f, 2));
+      d[4 * i + 3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(ws[i], 1.0f, 3));
+    }
+  }
+}
+
+// seg_dot on dequantised pairs: one chain of 16 dot2 in seg_dot's order.
+__device__ __forceinline__ float seg_dot_dq(const uint32_t (&d)[16], const uint32_t* xrow, int S, int s) {
+  float v = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint4 x = *reinterpret_cast<const uint4*>(xrow + (i * S + s) * 4);
+    v = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, d[4 * i + 0]), __builtin_bit_cast(bf16x2_t, x.x), v, false);
+    v = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, d[4 * i + 1]), __builtin_bit_cast(bf16x2_t, x.y), v, false);
+    v = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, d[4 * i + 2]), __builtin_bit_cast(bf16x2_t, x.z), v, false);
+    v = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, d[4 * i + 3]), __builtin_bit_cast(bf16x2_t, x.w), v, false);
+  }
+  return v;
+}
+
 // One-token kernel (decode1.hip): used by launch_fused for B = 1 when it
 // supports the shape (ZMOE_DECODE1=0 in the environment turns it off).
 bool decode1_supported(const zmoe_layer_desc* d, int grid);
