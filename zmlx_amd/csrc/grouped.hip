@@ -43,14 +43,15 @@ namespace zmoe {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-constexpr int kGThreads = 512;  // 8 waves
+constexpr int kGThreads = 256;  // 4 waves
 constexpr int kGWaves = kGThreads / 64;
 constexpr int kGTileN = 32 * kGWaves;  // output rows per workgroup
 constexpr int kGTileM = 32;            // sorted rows per MFMA block
-constexpr int kGBlocksM = 2;           // MFMA blocks per chunk
+constexpr int kGBlocksM = 1;           // MFMA blocks per chunk
 constexpr int kGChunk = kGTileM * kGBlocksM;
 constexpr int kGLdsRow = 64 + 8;       // bf16 per staged activation row (64 k + pad)
 constexpr int kGStage = kGChunk * 8 / kGThreads;  // 16-byte staging pieces per thread
+static_assert(kGChunk == kGroupedChunk && kGStage >= 1, "chunk");
 
 
 // ---------------------------------------------------------------------------
@@ -187,7 +188,7 @@ __host__ __device__ inline size_t grouped_pcache_bytes(int qmode, bool swiglu, i
 constexpr size_t kGPcacheMax = 96 * 1024;
 
 template <int QMODE, int GS, bool SWIGLU, bool PLDS, int NB>
-__global__ __launch_bounds__(kGThreads) void k_grouped_qmm(GroupedArgs g) {
+__global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(3, 8))) void k_grouped_qmm(GroupedArgs g) {
   __shared__ __align__(16) uint16_t alds[2][kGChunk * kGLdsRow];
   extern __shared__ __align__(16) unsigned char pcache[];
   constexpr bool G32 = GS == 32;
@@ -518,7 +519,7 @@ static void launch_grouped_t(hipStream_t st, const GroupedArgs& g, int n_experts
     static int nb = -1;
     if (nb < 0) {
       const char* e = getenv("ZMOE_GNB");
-      nb = e ? atoi(e) : 5;
+      nb = e ? atoi(e) : 4;
     }
     if constexpr (QMODE == ZMOE_Q_AFFINE && SWIGLU) {  // (mxfp4 would spill)
       if (nb == 4) return launch_grouped_nb<QMODE, GS, SWIGLU, true, 4>(st, g, blocks, pc);

@@ -39,10 +39,12 @@ bool grouped_params_cached(int quant_mode, bool swiglu, int K, int gs);
 // offsets[E+2] / sorted[npairs]: the pairs (token, k) in expert order;
 // blocks[]: every expert's chunks of `chunk` rows (at most npairs / chunk + E
 // of them; 64 for the MFMA GEMM, kGroupedGemvRows for the GEMV).
+// Sorted rows per chunk of the MFMA GEMM (one workgroup's rows).
+constexpr int kGroupedChunk = 32;
 int launch_sort_pairs(hipStream_t st, const uint32_t* idx, int npairs, int E, int* offsets, int* sorted, int* blocks,
-                      int chunk = 64);
-// Upper bound on the 64-row chunks of npairs pairs over E experts.
-inline int grouped_max_blocks(int npairs, int E) { return (npairs + 63) / 64 + E; }
+                      int chunk = kGroupedChunk);
+// Upper bound on the MFMA GEMM's chunks of npairs pairs over E experts.
+inline int grouped_max_blocks(int npairs, int E) { return (npairs + kGroupedChunk - 1) / kGroupedChunk + E; }
 
 // Expert-major GEMV (qmv.hip) for batches with few rows per expert: each
 // expert's weight rows are read once per chunk of kGroupedGemvRows sorted
