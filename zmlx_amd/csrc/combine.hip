@@ -94,8 +94,9 @@ __device__ __forceinline__ float combine_finish(int mode, float acc) {
 // KT = 0 takes K at run time (loads clamped to K - 1); WF32: f32 weights
 // (else bf16).
 constexpr int kCombVecMaxK = kCombMaxK;
+constexpr int kCombVecThreads = 256;
 template <int KT, bool WF32>
-__global__ __launch_bounds__(64) void k_moe_combine8(const uint16_t* __restrict__ y, const void* __restrict__ w,
+__global__ __launch_bounds__(256) void k_moe_combine8(const uint16_t* __restrict__ y, const void* __restrict__ w,
                                                       int w_dtype, int K, int D, int mode, int force_bf16,
                                                       const uint16_t* __restrict__ shared, void* __restrict__ out) {
   const int d0 = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
@@ -166,8 +167,8 @@ int launch_combine(hipStream_t st, const void* y, const void* w, int w_dtype, in
               : K == 2 ? (f ? k_moe_combine8<2, true> : k_moe_combine8<2, false>)
               : K == 1 ? (f ? k_moe_combine8<1, true> : k_moe_combine8<1, false>)
                        : (f ? k_moe_combine8<0, true> : k_moe_combine8<0, false>);
-    // one wave per 512 outputs, so small batches still spread over the CUs
-    hipLaunchKernelGGL(fn, dim3((D / 8 + 63) / 64, B), dim3(64), 0, st, static_cast<const uint16_t*>(y), w, w_dtype,
+    const int bt = kCombVecThreads;
+    hipLaunchKernelGGL(fn, dim3((D / 8 + bt - 1) / bt, B), dim3(bt), 0, st, static_cast<const uint16_t*>(y), w, w_dtype,
                        K, D, mode, force_bf16, static_cast<const uint16_t*>(shared), out);
   } else if (K <= kCombMaxK) {
     const bool f = w_dtype == ZMOE_DT_F32;
