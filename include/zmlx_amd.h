@@ -188,6 +188,29 @@ int zmoe_moe_combine(void* stream, const void* y, const void* w, int w_dtype, in
                      int D, int mode, void* out);
 
 /*
+ * Two-input SwiGLU out = SiLU(gate) * up, elementwise over n elements.
+ * Replaces transformer.swiglu2 (transformer.py:882-935).  dtype ZMOE_DT_BF16
+ * (MLX op-by-op rounding: sigmoid, gate*sigmoid and the product each rounded
+ * to bf16) or ZMOE_DT_F32; gate, up, out of that dtype.
+ */
+int zmoe_swiglu2(void* stream, const void* gate, const void* up, int64_t n, int dtype, void* out);
+
+/*
+ * Its backward (transformer.py:899-914): dgate = c*up*(s + g*s*(1 - s)),
+ * dup = c*g*s with s = sigmoid(gate), c = cotan; f32 arithmetic, one rounding
+ * to the dtype.
+ */
+int zmoe_swiglu2_backward(void* stream, const void* gate, const void* up, const void* cotan, int64_t n,
+                          int dtype, void* dgate, void* dup);
+
+/*
+ * Token-to-expert-slot copy out[b, k, :] = x[b, :] for k < K.  Replaces
+ * moe.moe_dispatch (moe.py:776-827; its indices only give K).  x: [B, D],
+ * out: [B, K, D], elements of elem_bytes (1, 2, 4 or 8) bytes.
+ */
+int zmoe_moe_dispatch(void* stream, const void* x, int64_t B, int D, int K, int elem_bytes, void* out);
+
+/*
  * Streaming combine step out = acc + gate[b] * proj[b, :] (moe.py:1820-1921,
  * used by gather_qmm_combine_quantized's streaming loop :2143-2172).
  * acc/out: bf16 or f32 (acc_dtype, same for both; in-place allowed);

@@ -255,6 +255,31 @@ def swiglu(g, u) -> np.ndarray:
     return bf16_round(silu * np.asarray(u, np.float32))
 
 
+def swiglu2_f32(g, u) -> np.ndarray:
+    """``transformer.swiglu2`` on float32 arrays (transformer.py:882-890,
+    917-935): ``g * kk_sigmoid(g) * u`` evaluated in float32."""
+    g = np.asarray(g, np.float32)
+    return ((g * sigmoid_abs_f32(g)).astype(np.float32) * np.asarray(u, np.float32)).astype(np.float32)
+
+
+def swiglu2_backward(g, u, cotan):
+    """Backward of ``swiglu2`` (transformer.py:899-914) in float64:
+    s = sigmoid(g), dgate = c*u*(s + g*s*(1 - s)), dup = c*g*s."""
+    g = np.asarray(g, np.float64)
+    u = np.asarray(u, np.float64)
+    c = np.asarray(cotan, np.float64)
+    s = 1.0 / (1.0 + np.exp(-g))
+    sw = g * s
+    return c * u * (s + sw * (1.0 - s)), c * sw
+
+
+def moe_dispatch(x, k: int) -> np.ndarray:
+    """``moe.moe_dispatch`` (moe.py:776-827): ``out[..., j, :] = x[..., :]``
+    for every slot j < k."""
+    x = np.asarray(x)
+    return np.repeat(x[..., None, :], int(k), axis=-2)
+
+
 def gather_qmm_swiglu(x, gw, gs, gb, uw, us, ub, lhs_indices, rhs_indices, *, group_size=64, bits=4, mode="affine"):
     """Unfused reference of ``mx.gather_qmm_swiglu`` (patch:695-800):
     ``silu(gather_qmm(gate)) * gather_qmm(up)``."""

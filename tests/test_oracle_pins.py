@@ -418,3 +418,46 @@ def test_layer_top1_unit_gate_is_gather_gemv():
         g = O.qmv(x[b], banks["gate"].deq(e))
         u = O.qmv(x[b], banks["up"].deq(e))
         np.testing.assert_array_equal(out[b], O.qmv(O.swiglu(g, u), banks["down"].deq(e)))
+
+
+def test_swiglu2_f32_closed_form():
+    """swiglu2 (f32) against the reference test's float64 formula
+    (test_fused_ops.py:69-83, rtol 1e-4) and tighter: f32 evaluation."""
+    rng = np.random.default_rng(5)
+    g = rng.standard_normal((4, 257)).astype(np.float32) * 4
+    u = rng.standard_normal((4, 257)).astype(np.float32)
+    ref = g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64))) * u
+    np.testing.assert_allclose(O.swiglu2_f32(g, u), ref, rtol=1e-6, atol=1e-7)
+    # special points: SiLU(0) = 0, large |g| saturates to g or 0
+    np.testing.assert_allclose(O.swiglu2_f32(np.float32([0.0, 30.0, -30.0]), np.float32([5.0, 2.0, 2.0])),
+                               [0.0, 60.0, -60.0 / (1 + np.exp(30.0))], rtol=1e-6, atol=0)
+
+
+def test_swiglu2_backward_finite_differences():
+    """The backward formula against central differences of the float64
+    forward: a dropped term or sign fails by far more than the tolerance."""
+    rng = np.random.default_rng(6)
+    g = rng.standard_normal(64) * 3
+    u = rng.standard_normal(64)
+    c = rng.standard_normal(64)
+    f = lambda gg, uu: gg / (1 + np.exp(-gg)) * uu  # noqa: E731
+    h = 1e-6
+    dg_fd = c * (f(g + h, u) - f(g - h, u)) / (2 * h)
+    du_fd = c * (f(g, u + h) - f(g, u - h)) / (2 * h)
+    dg, du = O.swiglu2_backward(g, u, c)
+    np.testing.assert_allclose(dg, dg_fd, rtol=1e-6, atol=1e-8)
+    np.testing.assert_allclose(du, du_fd, rtol=1e-6, atol=1e-8)
+
+
+def test_moe_dispatch_by_loop():
+    """moe_dispatch against the reference kernel's index formula
+    out[(b*K + k)*D + d] = x[b*D + d] (moe.py:785-795), written as loops."""
+    x = np.arange(3 * 5, dtype=np.int32).reshape(3, 5)
+    K = 4
+    got = O.moe_dispatch(x, K).reshape(-1)
+    want = np.empty(3 * K * 5, np.int32)
+    for b in range(3):
+        for k in range(K):
+            for d in range(5):
+                want[(b * K + k) * 5 + d] = x.reshape(-1)[b * 5 + d]
+    np.testing.assert_array_equal(got, want)

@@ -122,6 +122,9 @@ _SIGNATURES = {
     "zmoe_moe_combine": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p]),
     "zmoe_weighted_accumulate": (
         c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_i64, c_int, c_int, c_int, c_int, c_void_p]),
+    "zmoe_swiglu2": (c_int, [c_void_p, c_void_p, c_void_p, c_i64, c_int, c_void_p]),
+    "zmoe_swiglu2_backward": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_i64, c_int, c_void_p, c_void_p]),
+    "zmoe_moe_dispatch": (c_int, [c_void_p, c_void_p, c_i64, c_int, c_int, c_int, c_void_p]),
     "zmoe_moe_layer_workspace_size": (c_size_t, [ctypes.POINTER(LayerDesc), c_int]),
     "zmoe_moe_layer_trace_info": (
         c_size_t, [ctypes.POINTER(LayerDesc), c_int, ctypes.POINTER(c_int), ctypes.POINTER(c_int)]),

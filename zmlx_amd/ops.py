@@ -42,6 +42,7 @@ __all__ = [
     "router_argpartition_logits_topk",
     "deepseek_router_topk_sigmoid",
     "moe_dispatch",
+    "swiglu2",
     "moe_combine",
     "moe_combine_no_fma",
     "moe_combine_exact",
@@ -444,9 +445,58 @@ def deepseek_router_topk_sigmoid(
 
 def moe_dispatch(x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
     """Copy each token to its K expert slots: ``(..., D) -> (..., K, D)``
-    (moe.py:776-827; a pure broadcast copy)."""
+    (moe.py:776-827; the indices give K only)."""
+    op = "moe_dispatch"
+    dev = _require_gpu(op, x)
     K = int(indices.shape[-1])
-    return x.unsqueeze(-2).expand(*x.shape[:-1], K, x.shape[-1]).contiguous()
+    D = int(x.shape[-1])
+    xc = x.contiguous()
+    B = int(xc.numel() // max(1, D))
+    out = torch.empty((*x.shape[:-1], K, D), dtype=x.dtype, device=dev)
+    N.check(N.lib().zmoe_moe_dispatch(_stream(dev), _ptr(xc), B, D, K, xc.element_size(), _ptr(out)), op)
+    return out
+
+
+def _swiglu2_dtype(t: torch.Tensor, op: str) -> int:
+    if t.dtype == torch.bfloat16:
+        return N.DT_BF16
+    if t.dtype == torch.float32:
+        return N.DT_F32
+    raise ValueError(f"{op}: gate and up must be bfloat16 or float32 (got {t.dtype})")
+
+
+class _SwiGLU2(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, gate, up):
+        op = "swiglu2"
+        dev = _require_gpu(op, gate, up)
+        g, u = gate.contiguous(), up.contiguous()
+        out = torch.empty_like(g)
+        N.check(N.lib().zmoe_swiglu2(_stream(dev), _ptr(g), _ptr(u), g.numel(), _swiglu2_dtype(g, op), _ptr(out)),
+                op)
+        ctx.save_for_backward(g, u)
+        return out
+
+    @staticmethod
+    def backward(ctx, cotan):
+        op = "swiglu2"
+        g, u = ctx.saved_tensors
+        c = cotan.to(g.dtype).contiguous()
+        dg, du = torch.empty_like(g), torch.empty_like(u)
+        N.check(N.lib().zmoe_swiglu2_backward(_stream(g.device), _ptr(g), _ptr(u), _ptr(c), g.numel(),
+                                              _swiglu2_dtype(g, op), _ptr(dg), _ptr(du)), op)
+        return dg, du
+
+
+def swiglu2(gate: torch.Tensor, up: torch.Tensor, *, compute_dtype: Any | None = None) -> torch.Tensor:
+    """``SiLU(gate) * up`` with two separate inputs, differentiable
+    (transformer.py:917-935).  bf16 or f32; ``compute_dtype`` is accepted and
+    ignored, as the reference deprecates it."""
+    if gate.shape != up.shape:
+        raise ValueError("swiglu2: gate and up must have the same shape")
+    if gate.dtype != up.dtype:
+        raise ValueError("swiglu2: gate and up must have the same dtype")
+    return _SwiGLU2.apply(gate, up)
 
 
 def _combine(expert_outputs, weights, mode: int, op: str) -> torch.Tensor:
