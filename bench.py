@@ -323,14 +323,23 @@ def phase_trace(args) -> int:
     from zmlx_amd import _native as N
 
     dev = torch.device("cuda:0")
-    layers, _ = build_layers(dev, args.layers)
     gen = torch.Generator(device=dev)
     gen.manual_seed(1234)
     B = args.batch
     if B != 1:
-        print("--phase-trace: B=1 (the XCD-partitioned one-token kernel) only", file=sys.stderr)
+        print("--phase-trace: B=1 (the one-token kernels) only", file=sys.stderr)
         return 2
-    x = torch.randn((B, H), generator=gen, device=dev).to(torch.bfloat16)
+    if args.phase_config:
+        if args.phase_config not in OTHER_CONFIGS:
+            print(f"--phase-config: one of {sorted(OTHER_CONFIGS)}", file=sys.stderr)
+            return 2
+        layers = build_config_layers(args.phase_config, dev, gen)
+        hidden = OTHER_CONFIGS[args.phase_config][1]
+    else:
+        layers, _ = build_layers(dev, args.layers)
+        hidden = H
+    print(f"config: {args.phase_config or 'qwen3_30b_a3b'}")
+    x = torch.randn((B, hidden), generator=gen, device=dev).to(torch.bfloat16)
     phases = PHASES
     ms = time_layers(layers, x, args.steps, args.warmup)
     print(f"B={B} untraced: {ms * 1e3 / len(layers):.2f} us per layer call")
@@ -447,46 +456,56 @@ def expert_bytes(h, i, mode, gs) -> int:
     return 2 * i * (h // 2 + h // 32) + h * (i // 2 + i // 32)
 
 
-def other_config_lines(dev, steps: int, warmup: int) -> dict:
-    """Per-config lines: us per layer call, algorithmic GB/s and the fraction
-    of the 8 TB/s roofline at each of the config's batch sizes."""
+def build_config_layers(name: str, dev, g):
+    """The layer copies of one of OTHER_CONFIGS (random weights from g)."""
     import torch
 
     from zmlx_amd.layer import QuantizedMoELayer, QuantProj
     from zmlx_amd.quant import quantize_affine, quantize_mxfp4
 
+    fam, h, e, k, i, mode, gs, shi, kw, _, copies = OTHER_CONFIGS[name]
+    log(f"{name}: building {copies} layer copies")
+
+    def bank(n_exp, n_out, n_in):
+        ws, ss, bs = [], [], []
+        for e0 in range(0, n_exp, 16):
+            w = (torch.randn((min(16, n_exp - e0), n_out, n_in), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+            if mode == "affine":
+                q, sc, bi = quantize_affine(w, gs)
+            else:
+                (q, sc), bi = quantize_mxfp4(w), None
+            ws.append(q), ss.append(sc), bs.append(bi)
+        return torch.cat(ws), torch.cat(ss), (torch.cat(bs) if bs[0] is not None else None)
+
+    base = {"gate": bank(e, i, h), "up": bank(e, i, h), "down": bank(e, h, i)}
+    sh = {"gate": bank(1, shi, h), "up": bank(1, shi, h), "down": bank(1, h, shi)} if shi else None
+    layers = []
+    for _ in range(copies):
+        cp = {n: tuple(None if t is None else t.clone() for t in v) for n, v in base.items()}
+        shared = None
+        if sh is not None:
+            shared = tuple(QuantProj(v[0][0].clone(), v[1][0].clone(), None if v[2] is None else v[2][0].clone())
+                           for v in (sh["gate"], sh["up"], sh["down"]))
+        wr = (torch.randn((e, h), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        bias = (torch.randn((e,), generator=g, device=dev) * 0.05) if fam in ("glm", "deepseek") else None
+        layers.append(QuantizedMoELayer.for_family(
+            fam, wr, *(QuantProj(*cp[n]) for n in ("gate", "up", "down")), top_k=k, router_bias=bias,
+            group_size=gs, mode=mode, shared=shared, **kw))
+    del base, sh
+    torch.cuda.synchronize()
+    return layers
+
+
+def other_config_lines(dev, steps: int, warmup: int) -> dict:
+    """Per-config lines: us per layer call, algorithmic GB/s and the fraction
+    of the 8 TB/s roofline at each of the config's batch sizes."""
+    import torch
+
     out = {}
     g = torch.Generator(device=dev)
     g.manual_seed(77)
     for name, (fam, h, e, k, i, mode, gs, shi, kw, batches, copies) in OTHER_CONFIGS.items():
-        log(f"{name}: building {copies} layer copies")
-
-        def bank(n_exp, n_out, n_in):
-            ws, ss, bs = [], [], []
-            for e0 in range(0, n_exp, 16):
-                w = (torch.randn((min(16, n_exp - e0), n_out, n_in), generator=g, device=dev) * 0.02).to(torch.bfloat16)
-                if mode == "affine":
-                    q, sc, bi = quantize_affine(w, gs)
-                else:
-                    (q, sc), bi = quantize_mxfp4(w), None
-                ws.append(q), ss.append(sc), bs.append(bi)
-            return torch.cat(ws), torch.cat(ss), (torch.cat(bs) if bs[0] is not None else None)
-
-        base = {"gate": bank(e, i, h), "up": bank(e, i, h), "down": bank(e, h, i)}
-        sh = {"gate": bank(1, shi, h), "up": bank(1, shi, h), "down": bank(1, h, shi)} if shi else None
-        layers = []
-        for _ in range(copies):
-            cp = {n: tuple(None if t is None else t.clone() for t in v) for n, v in base.items()}
-            shared = None
-            if sh is not None:
-                shared = tuple(QuantProj(v[0][0].clone(), v[1][0].clone(), None if v[2] is None else v[2][0].clone())
-                               for v in (sh["gate"], sh["up"], sh["down"]))
-            wr = (torch.randn((e, h), generator=g, device=dev) * 0.02).to(torch.bfloat16)
-            bias = (torch.randn((e,), generator=g, device=dev) * 0.05) if fam in ("glm", "deepseek") else None
-            layers.append(QuantizedMoELayer.for_family(
-                fam, wr, *(QuantProj(*cp[n]) for n in ("gate", "up", "down")), top_k=k, router_bias=bias,
-                group_size=gs, mode=mode, shared=shared, **kw))
-        torch.cuda.synchronize()
+        layers = build_config_layers(name, dev, g)
         for B in batches:
             x = torch.randn((B, h), generator=g, device=dev).to(torch.bfloat16)
             uniq = []
@@ -504,7 +523,7 @@ def other_config_lines(dev, steps: int, warmup: int) -> dict:
                                    "unique_experts": round(avg_u, 2), "alg_bytes_per_call": int(alg),
                                    "layer_copies": copies, "steps": steps}
             log(f"{name} B={B}: {out[f'{name}_b{B}']}")
-        del layers, base, sh
+        del layers
         torch.cuda.empty_cache()
     return out
 
@@ -526,6 +545,8 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     ap.add_argument("--profile-run", action="store_true", help="short run for rocprofv3 counter passes")
     ap.add_argument("--phase-trace", action="store_true", help="per-phase stamps of the B=1 layer kernel")
+    ap.add_argument("--phase-config", default="", help="with --phase-trace: one of the other configs "
+                    "(e.g. lfm2_8b_a1b) instead of the Qwen3 layer")
     ap.add_argument("--summarize-pmc", nargs="+", metavar="PATH",
                     help="OUT_JSON FETCH_DIR WRITE_DIR [MFMA_DIR]: per-kernel counter summary")
     args = ap.parse_args()

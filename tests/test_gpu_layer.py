@@ -369,7 +369,8 @@ def test_layer_expert_major_gemv(dev, mode, gs):
 
 @pytest.mark.parametrize("family,shape,B", [
     ("qwen3", dict(H=2048, E=32, I=768, K=8), 1),     # XCD-partitioned one-token kernel
-    ("lfm2", dict(H=2048, E=32, I=1792, K=4), 1),     # one-token kernel
+    ("lfm2", dict(H=2048, E=32, I=1792, K=4), 1),     # the same, two XCDs per unit
+    ("qwen3", dict(H=2048, E=32, I=768, K=4), 1),     # one-token kernel (grid-wide exchanges)
     ("qwen3", dict(H=2048, E=32, I=768, K=8, shared_I=768), 4),  # batched kernel (shared expert)
 ])
 def test_wait_give_up_is_loud(dev, family, shape, B):

@@ -8,7 +8,9 @@
 // XCD costs a fraction of one across the chip.  When the layer has exactly 8
 // units (top-8 routing and no shared expert, or top-7 plus one) this kernel
 // gives the 32 workgroups of XCD x unit x, so that the only exchanges that
-// leave an XCD are the 8 unit outputs of each output row:
+// leave an XCD are the 8 unit outputs of each output row.  With 4 units
+// (LFM2-8B-A1B: top-4) two XCDs share a unit (R = 2): both compute all of
+// its gate/up rows, and XCD x computes output rows of half x % 2.
 //
 //   R  every XCD computes all router logits: one wave per router row, the
 //      chunk sums of k_dense_logits, one tagged word (bf16 | tag << 16) per
@@ -17,13 +19,13 @@
 //      routing keys to its own LDS copy; thread t ranks expert t / Q (as
 //      k_moe_decode1), and the expert of rank x becomes this XCD's unit;
 //   A  the XCD's 256 waves compute the unit's gate/up + SwiGLU rows (I / 256
-//      each) and store them, tagged, into the XCD's act row; each wave loads
-//      its down-projection items once its gate/up rows have arrived;
+//      each) and store them, tagged, into the XCD's act row; each wave then
+//      loads its down-projection items (its gate/up rows have arrived);
 //   D  every workgroup stages the act row from L2 (polling its tags) and
-//      computes its H / 32 output rows of the unit's down projection, stored
-//      as tagged words with device-scope stores;
-//   C  per 64-row chunk, the workgroup of the same index on XCD chunk % 8
-//      polls the 8 units' values and writes the k-ordered combine.
+//      computes its H / (32 R) output rows of the unit's down projection,
+//      stored as tagged words with device-scope stores;
+//   C  per chunk of output rows, one workgroup of the XCDs that computed
+//      them polls the units' values and writes the k-ordered combine.
 //
 // The layer shape is a template constant (hidden 2048 on a 256-CU device,
 // expert intermediate I_), so the work assignment is folded at compile time.
@@ -38,18 +40,29 @@
 
 namespace zmoe {
 
-template <int I_>
+// R XCDs share a unit (8 / R units): each computes all of the unit's gate/up
+// rows and H / R of its output rows.
+template <int I_, int R>
 struct D1XShape {
   static constexpr int H = kXH, S_H = kXH / 32, NC = kXH / 512;
   static constexpr int S_I = I_ / 32;
+  static constexpr int UX = kNX / R;                  // units
+  static constexpr int HR = H / R;                    // output rows per XCD
   static constexpr int RA = (I_ + kXWX - 1) / kXWX;   // gate/up rows per wave
-  static constexpr int RD = H / kXWX;                 // output rows per wave
+  static constexpr int RD = HR / kXWX;                // output rows per wave of the XCD
+  static constexpr int RW = RD * kFWaves;             // output rows per workgroup
   static constexpr int LI = cgcd(S_I, kWave);         // lanes per down row
   static constexpr int RPID = kWave / LI;             // down rows per load
   static constexpr int TD = S_I / LI;                 // segments per lane and row
-  static constexpr int ND = ((RD + RPID - 1) / RPID) * TD;  // down items per wave
-  static_assert(I_ % 32 == 0 && H % kXWX == 0, "shape");
-  static_assert(RA <= kD1A && ND <= kD1D && RD * kNX <= kWave, "work per wave");
+  // When a wave's share is below one load's rows, the workgroup's rows go to
+  // its last DW waves, RPID each (no lanes load a repeated row), and the
+  // other waves stage the act row with no down loads queued ahead of them.
+  static constexpr int DRW = RD >= RPID ? RD : RPID;  // rows per down wave
+  static constexpr int DW = RW / DRW;                 // down waves per workgroup
+  static constexpr int ND = ((DRW + RPID - 1) / RPID) * TD;  // down items per wave
+  static_assert(I_ % 32 == 0 && kNX % R == 0 && HR % kXWX == 0 && RW % DRW == 0, "shape");
+  static_assert(RA <= 8 && ND <= 8 && DRW * UX <= kWave, "work per wave");
+  static_assert(DW == kFWaves || S_I * 4 <= (kFWaves - DW) * kWave, "act staging outside the down waves");
 };
 
 struct D1XLayout {
@@ -101,9 +114,9 @@ struct D1XArgs {
   int route_kind, norm, w_bf16;
 };
 
-template <int QMODE, int P, int I_>
+template <int QMODE, int P, int I_, int R>
 __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
-  using S = D1XShape<I_>;
+  using S = D1XShape<I_, R>;
   constexpr D1XLayout lay = d1x_layout(I_);
   extern __shared__ __align__(16) unsigned char smem[];
   D1Lds& L = *reinterpret_cast<D1Lds*>(smem);
@@ -148,8 +161,10 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = __lane_id();
   // the workgroups on physical XCD `xcd` (g, g + 8, g + 16, ...) compute unit
-  // `xcd`; gi is the index among them
+  // ux = xcd / R and its output rows of part xcd % R; gi is the index among
+  // them
   const int xcd = xcc_id();
+  const int ux = xcd / R, hpart = xcd % R;
   const int gi = blockIdx.x / kNX;
   const int q = gi * kFWaves + wave;  // wave index within the XCD
   const AffineK ak = affine_k();
@@ -273,10 +288,10 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
   mark(5);
 
   // ---------------- A: gate/up + SwiGLU of unit xcd ----------------
-  // this XCD's unit: the expert of rank xcd, or the shared expert (unit K).
+  // this XCD's unit: the expert of rank ux, or the shared expert (unit K).
   // Clamped: after a wait gave up, the waves may have ranked different
-  // (stale) logits, and then no thread need have written rank xcd.
-  const int ue = xcd < K ? min(max(__builtin_amdgcn_readfirstlane(L.route.sel[xcd]), 0), E - 1) : -1;
+  // (stale) logits, and then no thread need have written rank ux.
+  const int ue = ux < K ? min(max(__builtin_amdgcn_readfirstlane(L.route.sel[ux]), 0), E - 1) : -1;
   const uint32_t* uw[3];
   const void* us[3];
   const void* ub[3];
@@ -288,7 +303,9 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
   }
   // down-projection items: lane group rs (of RPID) takes row h0 + g * RPID +
   // rs, lane li of it segments t * LI + li
-  const int h0 = q * S::RD;
+  const int dw = wave - (kFWaves - S::DW);  // index among the down waves, < 0: none
+  const bool dwave = dw >= 0;
+  const int h0 = hpart * S::HR + gi * S::RW + (dwave ? dw : 0) * S::DRW;
   const int rsD = lane / S::LI, liD = lane % S::LI;
   constexpr int64_t wprD = I_ / 8;
   const int pprD = (QMODE == ZMOE_Q_AFFINE) ? (S::S_I >> gshift) : S::S_I;
@@ -298,7 +315,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
 #pragma unroll
     for (int j = 0; j < S::ND; ++j) {
       const int g = j / S::TD, t = j % S::TD;
-      const int row = h0 + min(g * S::RPID + rsD, S::RD - 1);
+      const int row = h0 + min(g * S::RPID + rsD, S::DRW - 1);
       const int sgm = t * S::LI + liD;
       wd[j] = gload(reinterpret_cast<const uint4*>(uw[2] + row * wprD + sgm * 4));
       rd[j] = seg_param_load<QMODE>(us[2], ub[2], row * pprD + ((QMODE == ZMOE_Q_AFFINE) ? (sgm >> gshift) : sgm));
@@ -381,8 +398,10 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
     actw = (tag16 << 16) | (wg_dead() ? kBf16NaN : swiglu_bf16(round_bf16(gsel), round_bf16(usel)));
   }
   mark(6);
-  load_d();
+  // the act words leave before the down-projection loads of the same wave
+  // (LFM2 shape: act row staged 0.6 us earlier)
   if (lane < S::RA && a_r0 + lane < I_) gstore(act + static_cast<int64_t>(xcd) * act_stride + a_r0 + lane, actw);
+  if (dwave) load_d();
   mark(7);
 
   // ---------------- D: the unit's act row from L2, down projection ----------------
@@ -440,7 +459,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
   mark(8);
   lds_barrier();
   mark(9);
-  {
+  if (dwave) {
     float ysum[S::ND];
     float acc = 0.0f;
 #pragma unroll
@@ -458,7 +477,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
     for (int j = 0; j < S::ND; ++j) {
       const int g = j / S::TD, t = j % S::TD;
       const int hl = g * S::RPID + rsD;
-      if (t == S::TD - 1 && liD == 0 && hl < S::RD)
+      if (t == S::TD - 1 && liD == 0 && hl < S::DRW)
         dev_store(xy + static_cast<int64_t>(xcd) * kXH + h0 + hl,
                   (tag16 << 16) | (wg_dead() ? kBf16NaN : f32_to_bf16_bits(ysum[j])));
     }
@@ -466,13 +485,14 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
   mark(10);
 
   // ---------------- C: k-ordered combine of the chunk, on one XCD ----------------
-  // chunk = the 8 * RD output rows of the workgroups with index gi; each
-  // wave of the combining workgroup takes its own RD rows: lane k * RD + r
-  // polls unit k's value of row h0 + r.
-  if (xcd == gi % kNX) {
-    const int k = lane / S::RD, r = lane % S::RD;
-    const bool mine = k < kNX;
-    const uint32_t* src = xy + static_cast<int64_t>(mine ? k : 0) * kXH + h0 + r;
+  // chunk = the output rows of the workgroups with index gi on the XCDs of
+  // part hpart (one per unit); the one of unit gi % UX combines them, each
+  // down wave its own DRW rows: lane k * DRW + r polls unit k's value of row
+  // h0 + r, stored by XCD k * R + hpart.
+  if (ux == gi % S::UX && dwave) {
+    const int k = lane / S::DRW, r = lane % S::DRW;
+    const bool mine = k < S::UX;
+    const uint32_t* src = xy + static_cast<int64_t>((mine ? k : 0) * R + hpart) * kXH + h0 + r;
     uint32_t v = 0;
     for (unsigned spins = 0;; ++spins) {
       v = dev_load(src);
@@ -483,24 +503,27 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
       }
     }
     float* yw = yl + wave * kWave;
-    if (mine) yw[r * kNX + k] = bf16_bits_to_f32(v & 0xFFFFu);
+    if (mine) yw[r * S::UX + k] = bf16_bits_to_f32(v & 0xFFFFu);
     wave_lds_sync();
-    if (lane < S::RD) {
-      const float* yr = yw + lane * kNX;
+    if (lane < S::DRW) {
+      const float* yr = yw + lane * S::UX;
       const float* wk = L.route.w;
       float o = round_bf16(combine_one(cmode, K, [&](int kk) { return yr[kk]; }, [&](int kk) { return wk[kk]; }));
-      if (K < kNX) o = add_nofma(o, yr[K]);
+      if (K < S::UX) o = add_nofma(o, yr[K]);
       if (wg_dead()) o = kPoison;
       gstore(out + h0 + lane, static_cast<uint16_t>(f32_to_bf16_bits(o)));
     }
   }
   mark(12);
-  if (threadIdx.x == 0) {
-    dev_store(sync + kEpochWord + blockIdx.x, epoch + 1);
-    if (trace) {
+  if (threadIdx.x == 0) dev_store(sync + kEpochWord + blockIdx.x, epoch + 1);
+  if (trace) {
+    // the down-projection and combine stamps (10-12) come from the first
+    // down wave, the others from thread 0
+    const bool t0 = threadIdx.x == 0, td = dw == 0 && lane == 0;
 #pragma unroll
-      for (int i = 0; i < kTraceSlots; ++i)
-        if (tsr[i]) gstore(trace + blockIdx.x * kTraceSlots + i, tsr[i]);
+    for (int i = 0; i < kTraceSlots; ++i) {
+      const bool dslot = i == 10 || i == 11 || i == 12;
+      if (tsr[i] && (dslot ? td : t0)) gstore(trace + blockIdx.x * kTraceSlots + i, tsr[i]);
     }
   }
 }
@@ -517,8 +540,12 @@ static bool d1x_enabled() {
   return on == 1;
 }
 
-// Intermediate sizes with a compiled kernel (Qwen3-30B-A3B: 768; OLMoE: 1024).
-static bool d1x_inter_ok(int I) { return I == 768 || I == 1024; }
+// XCDs per unit of a layer with Uall units (8 units: 1; 4 units: 2), or 0.
+static int d1x_share(int Uall) { return (Uall == kNX) ? 1 : (Uall == kNX / 2 ? 2 : 0); }
+
+// Intermediate sizes with a compiled kernel: 8 units (Qwen3-30B-A3B: 768;
+// OLMoE: 1024); 4 units (LFM2-8B-A1B: 1792).
+static bool d1x_inter_ok(int I, int R) { return R == 1 ? (I == 768 || I == 1024) : (R == 2 && I == 1792); }
 
 size_t xcd_rpart_bytes(const zmoe_layer_desc* d) { return static_cast<size_t>(kNX + 1) * d->n_experts * 4; }
 size_t xcd_xy_bytes(const zmoe_layer_desc* d) { return static_cast<size_t>(kNX) * d->hidden * 4; }
@@ -565,19 +592,20 @@ static size_t d1x_lds_bytes(int I) {
 static bool d1x_shape_ok(const zmoe_layer_desc* d, int G) {
   if (!d1x_enabled() || G != kXG) return false;
   const int Uall = d->top_k + (d->shared_inter > 0 ? 1 : 0);
-  if (Uall != kNX || d->top_k > kMaxTopK) return false;
+  const int R = d1x_share(Uall);
+  if (R == 0 || d->top_k > kMaxTopK) return false;
   if (d->shared_inter > 0 && d->shared_inter != d->inter) return false;
-  if (d->hidden != kXH || !d1x_inter_ok(d->inter)) return false;
+  if (d->hidden != kXH || !d1x_inter_ok(d->inter, R)) return false;
   const bool rank_route = d->router_kind == ZMOE_ROUTER_SOFTMAX_PROBS ||
                           (d->router_kind == ZMOE_ROUTER_TOPK_LOGITS && d->router_bias == nullptr && d->norm_topk_prob);
   if (!rank_route || d->n_experts > kD1RankMaxE || d->n_experts > kXWX) return false;
   return d1x_lds_bytes(d->inter) <= 160 * 1024;
 }
 
-template <int QMODE, int P, int I_>
+template <int QMODE, int P, int I_, int R>
 static int launch_d1x_t(hipStream_t st, const D1XArgs& a) {
   static bool prepared = false;
-  const void* fn = reinterpret_cast<const void*>(&k_moe_decode1x<QMODE, P, I_>);
+  const void* fn = reinterpret_cast<const void*>(&k_moe_decode1x<QMODE, P, I_, R>);
   const size_t lds = d1x_lds_bytes(I_);
   if (!prepared) {
     (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
@@ -586,22 +614,23 @@ static int launch_d1x_t(hipStream_t st, const D1XArgs& a) {
   int occ = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, kFThreads, lds) != hipSuccess || occ < 1)
     return fail(ZMOE_EUNSUPPORTED, "[moe_layer] XCD-partitioned kernel cannot be resident on every CU");
-  hipLaunchKernelGGL((k_moe_decode1x<QMODE, P, I_>), dim3(kXG), dim3(kFThreads), lds, st, a);
+  hipLaunchKernelGGL((k_moe_decode1x<QMODE, P, I_, R>), dim3(kXG), dim3(kFThreads), lds, st, a);
   return check_launch("moe_layer(XCD-partitioned one-token launch)");
 }
 
-template <int QMODE, int I_>
+template <int QMODE, int I_, int R>
 static int launch_d1x_p(hipStream_t st, const D1XArgs& a) {
   switch (route_slots(a.E)) {
-    case 1: return launch_d1x_t<QMODE, 1, I_>(st, a);
-    case 2: return launch_d1x_t<QMODE, 2, I_>(st, a);
-    default: return launch_d1x_t<QMODE, 4, I_>(st, a);
+    case 1: return launch_d1x_t<QMODE, 1, I_, R>(st, a);
+    case 2: return launch_d1x_t<QMODE, 2, I_, R>(st, a);
+    default: return launch_d1x_t<QMODE, 4, I_, R>(st, a);
   }
 }
 
 template <int QMODE>
 static int launch_d1x_q(hipStream_t st, const D1XArgs& a, int I) {
-  return I == 768 ? launch_d1x_p<QMODE, 768>(st, a) : launch_d1x_p<QMODE, 1024>(st, a);
+  if (I == 1792) return launch_d1x_p<QMODE, 1792, 2>(st, a);
+  return I == 768 ? launch_d1x_p<QMODE, 768, 1>(st, a) : launch_d1x_p<QMODE, 1024, 1>(st, a);
 }
 
 int try_decode1x(hipStream_t st, const zmoe_layer_desc* d, const FusedParams& fp, int grid) {

@@ -539,7 +539,8 @@ static size_t off_act(const zmoe_layer_desc* d, int B) {
 }
 static size_t off_flags(const zmoe_layer_desc* d, int B) {
   const int stride = d->inter > d->shared_inter ? d->inter : d->shared_inter;
-  const size_t Ptot = static_cast<size_t>(B) * d->top_k + (d->shared_inter > 0 ? B : 0);
+  size_t Ptot = static_cast<size_t>(B) * d->top_k + (d->shared_inter > 0 ? B : 0);
+  if (B == 1 && Ptot < 8) Ptot = 8;  // the XCD-partitioned one-token kernel: one act row per XCD
   return align256(off_act(d, B) + Ptot * stride * 4);
 }
 static size_t off_trace(const zmoe_layer_desc* d, int B) {
