@@ -474,9 +474,48 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(3, 8)
     kloop(std::integral_constant<int, 2>{});
   else
     kloop(std::integral_constant<int, 1>{});
-  if (!active) return;
   // epilogue: element i of block mb is row mb*32 + (i/4)*8 + h*4 + i%4 of
   // the chunk, column n
+  static_assert(kGBlocksM == 1, "one MFMA block per chunk");
+  if (QMODE == ZMOE_Q_AFFINE && SWIGLU && g.asum_out != nullptr) {
+    // group sums of the chunk's bf16 outputs for the down projection's
+    // offset term: the 32 x 128 tile goes through LDS and one thread per
+    // (row, group) adds it in k_row_group_sums' order (8-element pieces in
+    // k order), so the sums are bit-identical to that kernel's
+    uint16_t* tl = alds[0];  // [32 rows][kGTileN] (the staging buffers are free after the k loop)
+    static_assert(kGTileM * kGTileN <= 2 * kGChunk * kGLdsRow, "tile fits the staging buffers");
+    __syncthreads();
+    if (active) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int rl = (i >> 2) * 8 + h * 4 + (i & 3);
+        tl[rl * kGTileN + wave * 32 + col] =
+            static_cast<uint16_t>(swiglu_bf16(round_bf16(tot0[0][i]), round_bf16(tot1[0][i])));
+      }
+    }
+    __syncthreads();
+    const int gpt = kGTileN / GS;  // groups per tile
+    const int Gn = g.N / GS;
+    for (int it = threadIdx.x; it < kGTileM * gpt; it += kGThreads) {
+      const int rl = it / gpt, gg = it - rl * gpt;
+      const int r = r_begin + rl;
+      const int n_first = tile * kGTileN + gg * GS;
+      if (r < r_end && n_first < g.N) {
+        const uint16_t* p = tl + rl * kGTileN + gg * GS;
+        float sv = 0.0f;
+        for (int j = 0; j < GS; j += 8) {
+          const uint4 v = *reinterpret_cast<const uint4*>(p + j);
+          sv += (bf16_bits_to_f32(v.x & 0xFFFFu) + bf16_bits_to_f32(v.x >> 16)) +
+                (bf16_bits_to_f32(v.y & 0xFFFFu) + bf16_bits_to_f32(v.y >> 16)) +
+                (bf16_bits_to_f32(v.z & 0xFFFFu) + bf16_bits_to_f32(v.z >> 16)) +
+                (bf16_bits_to_f32(v.w & 0xFFFFu) + bf16_bits_to_f32(v.w >> 16));
+        }
+        const int64_t orow = g.scatter ? static_cast<int64_t>(g.sorted[r]) : static_cast<int64_t>(r);
+        g.asum_out[orow * Gn + n_first / GS] = sv;
+      }
+    }
+  }
+  if (!active) return;
 #pragma unroll
   for (int mb = 0; mb < kGBlocksM; ++mb) {
 #pragma unroll

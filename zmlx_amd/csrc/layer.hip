@@ -227,11 +227,16 @@ static int run_sequence(void* stream, const zmoe_layer_desc* d, const void* x, i
   }
   ZMOE_REQUIRE(d->bits == 4, ZMOE_EUNSUPPORTED, "[moe_layer] only 4-bit weights.");
 
+  const SeqMode mode = seq_mode(d, B);
   // 1. router projection (bf16 logits, as the gate nn.Linear returns them)
   // (prefill batches on MFMA; decode batches keep the chunk order that the
-  // single-launch kernels reproduce)
-  rc = use_grouped(d, B) && H % 2048 == 0 ? launch_logits_mfma(st, x, d->router_w, B, E, H, ZMOE_DT_BF16, ws.logits)
-                         : zmoe_dense_logits(stream, x, d->router_w, B, E, H, ZMOE_DT_BF16, ws.logits);
+  // single-launch kernels reproduce).  At hidden 2048 the MFMA router also
+  // writes the grouped GEMM's x group sums.
+  const bool mfma_router = use_grouped(d, B) && H % 2048 == 0;
+  const bool xsum_fused = mfma_router && mode == kSeqMfma && d->quant_mode == ZMOE_Q_AFFINE && H == 2048;
+  rc = mfma_router ? launch_logits_mfma(st, x, d->router_w, B, E, H, ZMOE_DT_BF16, ws.logits,
+                                        xsum_fused ? ws.xsum : nullptr, d->group_size)
+                   : zmoe_dense_logits(stream, x, d->router_w, B, E, H, ZMOE_DT_BF16, ws.logits);
   if (rc) return rc;
   // 2. gating
   int w_dtype = ZMOE_DT_BF16;
@@ -246,7 +251,6 @@ static int run_sequence(void* stream, const zmoe_layer_desc* d, const void* x, i
   }
   if (rc) return rc;
   // 3. routed experts: gate/up + SwiGLU, then down
-  const SeqMode mode = seq_mode(d, B);
   if (mode == kSeqGemv) {
     // expert-major GEMV over the pairs sorted by expert; act and y stay in
     // pair order
@@ -298,7 +302,7 @@ static int run_sequence(void* stream, const zmoe_layer_desc* d, const void* x, i
     const bool affine = d->quant_mode == ZMOE_Q_AFFINE;
     rc = launch_sort_pairs(st, ws.idx, npairs, E, ws.offsets, ws.sorted, ws.blocks);
     if (rc) return rc;
-    if (affine) {
+    if (affine && !xsum_fused) {
       rc = launch_row_group_sums(st, static_cast<const uint16_t*>(x), H, B, H, d->group_size, ws.xsum);
       if (rc) return rc;
     }
@@ -325,12 +329,10 @@ static int run_sequence(void* stream, const zmoe_layer_desc* d, const void* x, i
     g.gs = d->group_size;
     g.out = static_cast<uint16_t*>(ws.act);
     g.ldo = I;
+    g.asum_out = affine ? ws.asum : nullptr;  // the act group sums of the down projection, from the epilogue
     rc = launch_grouped(st, g, E, d->quant_mode, true);
     if (rc) return rc;
-    if (affine) {
-      rc = launch_row_group_sums(st, static_cast<const uint16_t*>(ws.act), I, npairs, I, d->group_size, ws.asum);
-      if (rc) return rc;
-    }
+    g.asum_out = nullptr;
     g.a = static_cast<const uint16_t*>(ws.act);
     g.lda = I;
     g.asum = ws.asum;

@@ -234,10 +234,19 @@ typedef __bf16 lg_bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float lg_f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kLgSteps = 4;  // k-steps of 32 per load batch
 constexpr int kLgWaves = 8;  // waves per tile, each a k range
+constexpr int kLgPieces = 32;  // 8-element pieces of one wave's k range (hidden 2048) with group sums
 
+// With xsum (affine grouped GEMMs), the workgroups of the first expert tile
+// also write the fp32 sums of every gs-group of their 16 token rows,
+// xsum[b][H / gs], from the x values they hold: each lane's 8 consecutive
+// values are summed as k_row_group_sums sums an 8-element piece, the pieces
+// of a group are then added in k order, so the sums are bit-identical to
+// k_row_group_sums'.
 __global__ __launch_bounds__(512) void k_logits_mfma(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-                                                     int B, int E, int H, int out_f32, void* __restrict__ out) {
+                                                     int B, int E, int H, int out_f32, void* __restrict__ out,
+                                                     float* __restrict__ xsum, int gs) {
   __shared__ float red[kLgWaves - 1][kWave][5];
+  __shared__ float piece[kLgWaves][16][kLgPieces + 1];  // 8-element sums: [wave][token][piece]
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int q = lane >> 4, col = lane & 15;  // k quarter (8 of every 32 k), row in the tile
   const int b0 = blockIdx.x * 16, e0 = blockIdx.y * 16;
@@ -246,6 +255,7 @@ __global__ __launch_bounds__(512) void k_logits_mfma(const uint16_t* __restrict_
   const uint16_t* xp = x + xr * H + wave * kq + q * 8;
   const uint16_t* wp = w + wr * H + wave * kq + q * 8;
   const int nch = kq / (32 * kLgSteps);  // load batches per wave (even)
+  const bool sums = xsum != nullptr && blockIdx.y == 0;
   lg_f32x4_t acc = {};
   // two register buffers in ping-pong, loads issued unconditionally (the
   // batch index clamped) so the compiler's wait counts stay exact
@@ -257,24 +267,47 @@ __global__ __launch_bounds__(512) void k_logits_mfma(const uint16_t* __restrict_
       wv[i] = gload(reinterpret_cast<const uint4*>(wp + (c * kLgSteps + i) * 32));
     }
   };
-  auto mfma = [&](const uint4* xv, const uint4* wv) {
+  auto mfma = [&](const uint4* xv, const uint4* wv, int c) {
 #pragma unroll
     for (int i = 0; i < kLgSteps; ++i)
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(lg_bf16x8_t, xv[i]),
                                                     __builtin_bit_cast(lg_bf16x8_t, wv[i]), acc, 0, 0, 0);
+    if (sums) {
+      // piece (c * kLgSteps + i) * 4 + q of this wave's k range: elements
+      // wave * kq + (c * kLgSteps + i) * 32 + q * 8 .. + 7 of token col
+#pragma unroll
+      for (int i = 0; i < kLgSteps; ++i) {
+        const uint4 v = xv[i];
+        const float t = (((bf16_bits_to_f32(v.x & 0xFFFFu) + bf16_bits_to_f32(v.x >> 16)) +
+                          (bf16_bits_to_f32(v.y & 0xFFFFu) + bf16_bits_to_f32(v.y >> 16))) +
+                         (bf16_bits_to_f32(v.z & 0xFFFFu) + bf16_bits_to_f32(v.z >> 16))) +
+                        (bf16_bits_to_f32(v.w & 0xFFFFu) + bf16_bits_to_f32(v.w >> 16));
+        piece[wave][col][(c * kLgSteps + i) * 4 + q] = t;
+      }
+    }
   };
   load(xa, wa, 0);
   for (int c = 0; c < nch; c += 2) {
     load(xb, wb, c + 1);
-    mfma(xa, wa);
+    mfma(xa, wa, c);
     load(xa, wa, min(c + 2, nch - 1));
-    mfma(xb, wb);
+    mfma(xb, wb, c + 1);
   }
   if (wave > 0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[wave - 1][lane][i] = acc[i];
   }
   __syncthreads();
+  if (sums) {
+    // this wave's kq / gs groups of the 16 tokens, pieces added in k order
+    const int ppg = gs / 8, gpw = kq / gs;
+    for (int it = lane; it < 16 * gpw; it += kWave) {
+      const int tok = it & 15, gg = it >> 4;
+      float sv = 0.0f;
+      for (int j = 0; j < ppg; ++j) sv += piece[wave][tok][gg * ppg + j];
+      if (b0 + tok < B) xsum[static_cast<int64_t>(b0 + tok) * (H / gs) + wave * gpw + gg] = sv;
+    }
+  }
   if (wave != 0) return;
   // element i of the 16x16 tile: token row 4*q + i, expert column col
 #pragma unroll
@@ -294,13 +327,15 @@ __global__ __launch_bounds__(512) void k_logits_mfma(const uint16_t* __restrict_
 }
 
 int zmoe::launch_logits_mfma(hipStream_t st, const void* x, const void* w, int B, int E, int H, int out_dtype,
-                             void* out) {
+                             void* out, float* xsum, int gs) {
   ZMOE_REQUIRE(H % (2 * kLgWaves * kLgSteps * 32) == 0, ZMOE_EINVAL_SHAPE,
                "[dense_logits] hidden must be a multiple of 2048.");
+  ZMOE_REQUIRE(xsum == nullptr || ((gs == 32 || gs == 64 || gs == 128) && H / kLgWaves <= kLgPieces * 8),
+               ZMOE_EINVAL_SHAPE, "[dense_logits] group sums: gs 32, 64 or 128 and hidden at most 2048.");
   if (B == 0) return ZMOE_OK;
   hipLaunchKernelGGL(k_logits_mfma, dim3((B + 15) / 16, (E + 15) / 16), dim3(kLgWaves * kWave), 0, st,
                      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), B, E, H,
-                     out_dtype == ZMOE_DT_F32 ? 1 : 0, out);
+                     out_dtype == ZMOE_DT_F32 ? 1 : 0, out, xsum, gs);
   return check_launch("dense_logits (mfma)");
 }
 

@@ -28,6 +28,7 @@ struct GroupedArgs {
   int N, K, gs;
   uint16_t* out;         // bf16 [rows][ldo]
   int64_t ldo;
+  float* asum_out;       // affine SwiGLU (optional): [out rows][N/gs] group sums of the bf16 outputs
 };
 
 // k_grouped_qmm over every expert's sorted rows; SwiGLU of two matrices when

@@ -50,7 +50,10 @@ int dispatch_qmv(bool swiglu, void* stream, const void* x, const uint32_t* wg, c
 int launch_combine(hipStream_t st, const void* y, const void* w, int w_dtype, int B, int K, int D, int mode,
                    int force_bf16, const void* shared, void* out);
 // router projection on MFMA (prefill batches; router.hip)
-int launch_logits_mfma(hipStream_t st, const void* x, const void* w, int B, int E, int H, int out_dtype, void* out);
+// With xsum: also the fp32 sums of every gs-group of each row of x,
+// xsum[B][H / gs] (hidden 2048), bit-identical to k_row_group_sums'.
+int launch_logits_mfma(hipStream_t st, const void* x, const void* w, int B, int E, int H, int out_dtype, void* out,
+                       float* xsum = nullptr, int gs = 64);
 int launch_topk_gating(hipStream_t st, const void* logits, int in_dtype, int B, int E, int k, const float* bias,
                        int norm, int out_bf16, void* out_w, uint32_t* out_idx);
 int launch_deepseek_router(hipStream_t st, const void* logits, int in_dtype, const float* bias, int B, int E, int k,
