@@ -371,6 +371,7 @@ def test_layer_expert_major_gemv(dev, mode, gs):
     ("qwen3", dict(H=2048, E=32, I=768, K=8), 1),     # XCD-partitioned one-token kernel
     ("lfm2", dict(H=2048, E=32, I=1792, K=4), 1),     # the same, two XCDs per unit
     ("qwen3", dict(H=2048, E=32, I=768, K=4), 1),     # one-token kernel (grid-wide exchanges)
+    ("glm", dict(H=2048, E=64, I=1536, K=4, mode="mxfp4", gs=32, shared_I=1536), 1),  # XCD kernel, 3 idle XCDs
     ("qwen3", dict(H=2048, E=32, I=768, K=8, shared_I=768), 4),  # batched kernel (shared expert)
 ])
 def test_wait_give_up_is_loud(dev, family, shape, B):
@@ -387,7 +388,13 @@ def test_wait_give_up_is_loud(dev, family, shape, B):
 
     rng = np.random.default_rng(31)
     banks, wr, sh, tq, tsh, wr_t = _build(dev, rng, **shape)
-    layer = QuantizedMoELayer.for_family(family, wr_t, tq["gate"], tq["up"], tq["down"], top_k=shape["K"], shared=tsh)
+    kw = {}
+    if family == "glm":
+        bias = (rng.standard_normal(shape["E"]) * 0.05).astype(np.float32)
+        kw = dict(router_bias=torch.from_numpy(bias).to(dev), group_size=shape["gs"], mode=shape["mode"],
+                  routed_scaling_factor=1.8)
+    layer = QuantizedMoELayer.for_family(family, wr_t, tq["gate"], tq["up"], tq["down"], top_k=shape["K"], shared=tsh,
+                                         **kw)
     assert layer._single_launch(B)
     x = to_bf16(bf16_randn(rng, (B, shape["H"])), dev)
     print(f"[give-up] {family} B={B}", flush=True)

@@ -64,36 +64,6 @@ __host__ __device__ inline D1Layout d1_layout(int H, int I, int E, int Uall, int
   return o;
 }
 
-// Rank of 64-bit key i (number of larger keys; keys are unique) over an
-// EPAD-entry row, Q = 512/EPAD adjacent threads per key, each counting one
-// slice in chunks of up to 16 keys.  Returns the rank in thread q == 0 of each
-// group (-1 elsewhere).
-template <int EPAD>
-__device__ __forceinline__ int rank_in_row64(const uint64_t* keys, int& i, uint64_t& ki) {
-  constexpr int Q = kFThreads / EPAD;
-  constexpr int PER = EPAD / Q;
-  constexpr int CH = PER < 16 ? PER : 16;  // keys per chunk
-  static_assert(Q >= 2 && Q <= 8 && PER % CH == 0 && CH % 2 == 0, "rank slices");
-  i = threadIdx.x / Q;
-  const int q = threadIdx.x % Q;
-  ki = keys[i];
-  int cnt = 0;
-  for (int c = 0; c < PER; c += CH) {
-    uint4 kk[CH / 2];
-#pragma unroll
-    for (int m = 0; m < CH / 2; ++m) kk[m] = *reinterpret_cast<const uint4*>(&keys[q * PER + c + 2 * m]);
-#pragma unroll
-    for (int m = 0; m < CH / 2; ++m) {
-      cnt += ((static_cast<uint64_t>(kk[m].y) << 32 | kk[m].x) > ki) ? 1 : 0;
-      cnt += ((static_cast<uint64_t>(kk[m].w) << 32 | kk[m].z) > ki) ? 1 : 0;
-    }
-  }
-  cnt += __builtin_amdgcn_update_dpp(0, cnt, kDppQuadSwap1, 0xF, 0xF, false);
-  if (Q >= 4) cnt += __builtin_amdgcn_update_dpp(0, cnt, kDppQuadSwap2, 0xF, 0xF, false);
-  if (Q >= 8) cnt += __builtin_amdgcn_update_dpp(0, cnt, kDppHalfMirror, 0xF, 0xF, false);
-  return q == 0 ? cnt : -1;
-}
-
 // Grouped sigmoid router (moe.py:1501-1742, deepseek_router.py:118) for
 // E = 64 P experts, groups of 32 (or no group limit), wave 0: the selection
 // scores sigmoid + bias with the dropped groups' scores set to 0, as unique

@@ -40,13 +40,14 @@
 
 namespace zmoe {
 
-// R XCDs share a unit (8 / R units): each computes all of the unit's gate/up
-// rows and H / R of its output rows.
-template <int I_, int R>
+// UX units, R XCDs per unit (UX * R <= 8; XCDs past UX * R idle): each
+// computes all of its unit's gate/up rows and H / R of its output rows.
+template <int I_, int R, int UX_>
 struct D1XShape {
   static constexpr int H = kXH, S_H = kXH / 32, NC = kXH / 512;
   static constexpr int S_I = I_ / 32;
-  static constexpr int UX = kNX / R;                  // units
+  static constexpr int UX = UX_;                      // units
+  static_assert(UX * R <= kNX, "units x XCDs per unit");
   static constexpr int HR = H / R;                    // output rows per XCD
   static constexpr int RA = (I_ + kXWX - 1) / kXWX;   // gate/up rows per wave
   static constexpr int RD = HR / kXWX;                // output rows per wave of the XCD
@@ -66,7 +67,7 @@ struct D1XShape {
 };
 
 struct D1XLayout {
-  size_t xs, as, asx, yl, keys, total;
+  size_t xs, as, asx, yl, keys, aux, total;
 };
 
 __host__ __device__ constexpr D1XLayout d1x_layout(int I) {
@@ -81,8 +82,10 @@ __host__ __device__ constexpr D1XLayout d1x_layout(int I) {
   off = (off + 15) & ~static_cast<size_t>(15);
   o.yl = off;
   off += static_cast<size_t>(kFWaves) * kWave * 4;
-  o.keys = off;  // one copy of the routing keys per wave
+  o.keys = off;  // one copy of the routing keys per wave (64-bit keys: E <= 128)
   off += static_cast<size_t>(kFWaves) * kD1RankMaxE * 4;
+  o.aux = off;   // sigmoid router: one copy of the sigmoids per wave
+  off += static_cast<size_t>(kFWaves) * 128 * 4;
   o.total = off;
   return o;
 }
@@ -112,11 +115,15 @@ struct D1XArgs {
   unsigned spin;           // polls before a wait gives up
   int E, K, gshift, combine_mode, act_stride;
   int route_kind, norm, w_bf16;
+  const float* rbias;      // sigmoid router: per-expert selection bias
+  float rscale;            // sigmoid router: routed scaling factor
 };
 
-template <int QMODE, int P, int I_, int R>
+// SIG: the sigmoid router (compiled only for the shapes that use it, so the
+// other kernels carry none of its code).
+template <int QMODE, int P, int I_, int R, int UX, bool SIG>
 __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
-  using S = D1XShape<I_, R>;
+  using S = D1XShape<I_, R, UX>;
   constexpr D1XLayout lay = d1x_layout(I_);
   extern __shared__ __align__(16) unsigned char smem[];
   D1Lds& L = *reinterpret_cast<D1Lds*>(smem);
@@ -155,8 +162,13 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
   unsigned spin = a.spin;
   ZMOE_PIN(err_host); ZMOE_PIN(spin);
   int cmode = a.combine_mode, act_stride = a.act_stride, rkind = a.route_kind, norm = a.norm, wbf = a.w_bf16;
+  const float* rbias = SIG ? a.rbias : nullptr;
+  float rscale = SIG ? a.rscale : 1.0f;
   ZMOE_PIN(act); ZMOE_PIN(xy); ZMOE_PIN(out); ZMOE_PIN(out_idx); ZMOE_PIN(out_w); ZMOE_PIN(trace);
   ZMOE_PIN(cmode); ZMOE_PIN(act_stride); ZMOE_PIN(rkind); ZMOE_PIN(norm); ZMOE_PIN(wbf);
+  if constexpr (SIG) {
+    ZMOE_PIN(rbias); ZMOE_PIN(rscale);
+  }
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = __lane_id();
@@ -182,6 +194,23 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
   const unsigned epoch = dev_load(sync + kEpochWord + blockIdx.x);
   const unsigned tag16 = (epoch + 1u) & 0xFFFFu;
   bool dead = false;  // a wait of this thread gave up (later waits give up at once)
+  if (UX * R < kNX && ux >= UX) {  // an XCD without a unit: only its launch count advances
+    if (threadIdx.x == 0) {
+      dev_store(sync + kEpochWord + blockIdx.x, epoch + 1);
+      if (trace) gstore(trace + blockIdx.x * kTraceSlots, tsr[0]);
+    }
+    return;
+  }
+  // the workgroup that writes the routing outputs (on an XCD with a unit)
+  const bool writer = (UX * R == kNX) ? blockIdx.x == 0 : (xcd == 0 && gi == 0);
+  // sigmoid router (moe.py:1501-1742, no group limit): selection scores are
+  // sigmoid + bias; the bias is loaded before the logits are waited for
+  constexpr bool sig = SIG;
+  float bv[P];
+  if constexpr (SIG) {
+#pragma unroll
+    for (int i = 0; i < P; ++i) bv[i] = lane + 64 * i < E ? gload(rbias + lane + 64 * i) : 0.0f;
+  }
 
   // ---------------- R: router logits, XCD-local ----------------
   uint32_t* lg = lg0 + E * (1 + xcd);
@@ -234,6 +263,8 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
   // barrier sits between the logits and the ranks.
   const int Epad = E <= 64 ? 64 : (E <= 128 ? 128 : 256);
   uint32_t* keys = reinterpret_cast<uint32_t*>(smem + lay.keys) + wave * Epad;
+  uint64_t* keys64 = reinterpret_cast<uint64_t*>(smem + lay.keys) + wave * Epad;  // sigmoid router (E <= 128)
+  float* aux = reinterpret_cast<float*>(smem + lay.aux) + wave * 128;
   {
     RowVals<P> row;
     for (unsigned n = 0;; ++n) {
@@ -263,14 +294,40 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
 #pragma unroll
       for (int i = 0; i < P; ++i) v[i] = div_to_bf16(v[i], sum);
     }
+    if constexpr (SIG) {
+      // unique 64-bit keys (score order key << 32 | ~e: value descending,
+      // then lower index), the ranking decode1.hip's grouped sigmoid path
+      // uses; the sigmoids beside them
 #pragma unroll
-    for (int i = 0; i < P; ++i) {
-      const int e = lane + 64 * i;
-      if (e < Epad) keys[e] = e < E ? ((order_key(v[i]) & 0xFFFF0000u) | (0xFFFFu - static_cast<uint32_t>(e))) : 0u;
+      for (int i = 0; i < P; ++i) {
+        const int e = lane + 64 * i;
+        const float sg = sigmoid_abs(v[i]);
+        if (e < Epad) {
+          keys64[e] = e < E ? (static_cast<uint64_t>(order_key(sg + bv[i])) << 32 |
+                               (0xFFFFFFFFu - static_cast<uint32_t>(e)))
+                            : 0ull;
+          aux[e] = sg;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < P; ++i) {
+        const int e = lane + 64 * i;
+        if (e < Epad) keys[e] = e < E ? ((order_key(v[i]) & 0xFFFF0000u) | (0xFFFFu - static_cast<uint32_t>(e))) : 0u;
+      }
     }
   }
   wave_lds_sync();
-  {
+  if constexpr (SIG) {
+    int i, r;
+    uint64_t kl;
+    if (Epad == 64) r = rank_in_row64<64>(keys64, i, kl);
+    else r = rank_in_row64<128>(keys64, i, kl);
+    if (r >= 0 && i < E && r < K) {
+      L.route.sel[r] = i;
+      L.route.saux[r] = aux[i];
+    }
+  } else {
     int i, r;
     uint32_t ki;
     if (Epad == 64) r = rank_in_row<64>(keys, i, ki);
@@ -342,9 +399,15 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
   // gate weights of the ranked winners (wave 0, lane r = winner r), for the
   // combine, and the routing outputs of workgroup 0
   if (wave == 0) {
-    const float val = lane < K ? L.route.sval[lane] : 0.0f;
+    const float val = lane < K ? (sig ? L.route.saux[lane] : L.route.sval[lane]) : 0.0f;
     float w;
-    if (rkind == kRouteSoftmaxProbs) {
+    if constexpr (SIG) {
+      // the sigmoids normalised in selection order, scaled (decode1.hip
+      // sig_weights, route_row's weights)
+      const float sum = ordered_lane_sum(val, K);
+      w = val / sum;
+      if (rscale != 1.0f) w = w * rscale;
+    } else if (rkind == kRouteSoftmaxProbs) {
       const float sb = round_bf16(ordered_lane_sum(val, K));
       w = norm ? div_to_bf16(val, sb) : val;
     } else {
@@ -357,7 +420,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1x(D1XArgs a) {
     }
     if (lane < K) {
       L.route.w[lane] = w;
-      if (blockIdx.x == 0) {
+      if (writer) {
         if (out_idx) gstore(out_idx + lane, static_cast<uint32_t>(L.route.sel[lane]));
         if (out_w) gstore(out_w + lane, w);
       }
@@ -540,12 +603,22 @@ static bool d1x_enabled() {
   return on == 1;
 }
 
-// XCDs per unit of a layer with Uall units (8 units: 1; 4 units: 2), or 0.
-static int d1x_share(int Uall) { return (Uall == kNX) ? 1 : (Uall == kNX / 2 ? 2 : 0); }
+// XCDs per unit of a layer with Uall units: 8 units: 1; 4 units: 2; 5 to 7
+// units: 1 (the other XCDs idle); else 0.
+static int d1x_share(int Uall) {
+  if (Uall == kNX / 2) return 2;
+  return (Uall >= 5 && Uall <= kNX) ? 1 : 0;
+}
 
-// Intermediate sizes with a compiled kernel: 8 units (Qwen3-30B-A3B: 768;
-// OLMoE: 1024); 4 units (LFM2-8B-A1B: 1792).
-static bool d1x_inter_ok(int I, int R) { return R == 1 ? (I == 768 || I == 1024) : (R == 2 && I == 1792); }
+// Shapes with a compiled kernel (expert intermediate, XCDs per unit, units,
+// router): Qwen3-30B-A3B (768, 1, 8), OLMoE (1024, 1, 8), LFM2-8B-A1B (1792,
+// 2, 4), ranked softmax or top-k logits; GLM-4.7-Flash-like (1536, 1, 5: 4
+// routed + 1 shared), sigmoid router.
+static bool d1x_inter_ok(int I, int R, int UX, bool sig) {
+  if (R == 1 && UX == kNX) return !sig && (I == 768 || I == 1024);
+  if (R == 2 && UX == 4) return !sig && I == 1792;
+  return R == 1 && UX == 5 && I == 1536 && sig;
+}
 
 size_t xcd_rpart_bytes(const zmoe_layer_desc* d) { return static_cast<size_t>(kNX + 1) * d->n_experts * 4; }
 size_t xcd_xy_bytes(const zmoe_layer_desc* d) { return static_cast<size_t>(kNX) * d->hidden * 4; }
@@ -595,17 +668,20 @@ static bool d1x_shape_ok(const zmoe_layer_desc* d, int G) {
   const int R = d1x_share(Uall);
   if (R == 0 || d->top_k > kMaxTopK) return false;
   if (d->shared_inter > 0 && d->shared_inter != d->inter) return false;
-  if (d->hidden != kXH || !d1x_inter_ok(d->inter, R)) return false;
   const bool rank_route = d->router_kind == ZMOE_ROUTER_SOFTMAX_PROBS ||
                           (d->router_kind == ZMOE_ROUTER_TOPK_LOGITS && d->router_bias == nullptr && d->norm_topk_prob);
-  if (!rank_route || d->n_experts > kD1RankMaxE || d->n_experts > kXWX) return false;
+  // the sigmoid router without a group limit, ranked over 64-bit keys (E <= 128)
+  const bool sig_route = d->router_kind == ZMOE_ROUTER_SIGMOID_GROUPED && d->router_bias != nullptr &&
+                         (d->n_group <= 1 || d->topk_group >= d->n_group) && d->n_experts <= 128;
+  if (!(rank_route || sig_route) || d->n_experts > kD1RankMaxE || d->n_experts > kXWX) return false;
+  if (d->hidden != kXH || !d1x_inter_ok(d->inter, R, Uall, sig_route)) return false;
   return d1x_lds_bytes(d->inter) <= 160 * 1024;
 }
 
-template <int QMODE, int P, int I_, int R>
+template <int QMODE, int P, int I_, int R, int UX, bool SIG>
 static int launch_d1x_t(hipStream_t st, const D1XArgs& a) {
   static bool prepared = false;
-  const void* fn = reinterpret_cast<const void*>(&k_moe_decode1x<QMODE, P, I_, R>);
+  const void* fn = reinterpret_cast<const void*>(&k_moe_decode1x<QMODE, P, I_, R, UX, SIG>);
   const size_t lds = d1x_lds_bytes(I_);
   if (!prepared) {
     (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
@@ -614,23 +690,26 @@ static int launch_d1x_t(hipStream_t st, const D1XArgs& a) {
   int occ = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, kFThreads, lds) != hipSuccess || occ < 1)
     return fail(ZMOE_EUNSUPPORTED, "[moe_layer] XCD-partitioned kernel cannot be resident on every CU");
-  hipLaunchKernelGGL((k_moe_decode1x<QMODE, P, I_, R>), dim3(kXG), dim3(kFThreads), lds, st, a);
+  hipLaunchKernelGGL((k_moe_decode1x<QMODE, P, I_, R, UX, SIG>), dim3(kXG), dim3(kFThreads), lds, st, a);
   return check_launch("moe_layer(XCD-partitioned one-token launch)");
 }
 
-template <int QMODE, int I_, int R>
+template <int QMODE, int I_, int R, int UX, bool SIG>
 static int launch_d1x_p(hipStream_t st, const D1XArgs& a) {
   switch (route_slots(a.E)) {
-    case 1: return launch_d1x_t<QMODE, 1, I_, R>(st, a);
-    case 2: return launch_d1x_t<QMODE, 2, I_, R>(st, a);
-    default: return launch_d1x_t<QMODE, 4, I_, R>(st, a);
+    case 1: return launch_d1x_t<QMODE, 1, I_, R, UX, SIG>(st, a);
+    case 2: return launch_d1x_t<QMODE, 2, I_, R, UX, SIG>(st, a);
+    default:
+      if constexpr (SIG) return fail(ZMOE_EUNSUPPORTED, "[moe_layer] XCD-partitioned sigmoid routing: E <= 128");
+      else return launch_d1x_t<QMODE, 4, I_, R, UX, SIG>(st, a);
   }
 }
 
 template <int QMODE>
 static int launch_d1x_q(hipStream_t st, const D1XArgs& a, int I) {
-  if (I == 1792) return launch_d1x_p<QMODE, 1792, 2>(st, a);
-  return I == 768 ? launch_d1x_p<QMODE, 768, 1>(st, a) : launch_d1x_p<QMODE, 1024, 1>(st, a);
+  if (I == 1792) return launch_d1x_p<QMODE, 1792, 2, 4, false>(st, a);
+  if (I == 1536) return launch_d1x_p<QMODE, 1536, 1, 5, true>(st, a);
+  return I == 768 ? launch_d1x_p<QMODE, 768, 1, kNX, false>(st, a) : launch_d1x_p<QMODE, 1024, 1, kNX, false>(st, a);
 }
 
 int try_decode1x(hipStream_t st, const zmoe_layer_desc* d, const FusedParams& fp, int grid) {
@@ -669,6 +748,8 @@ int try_decode1x(hipStream_t st, const zmoe_layer_desc* d, const FusedParams& fp
   a.route_kind = fp.route.kind;
   a.norm = fp.route.norm;
   a.w_bf16 = fp.route.w_bf16;
+  a.rbias = fp.route.bias;
+  a.rscale = fp.route.scale;
   if (d->quant_mode == ZMOE_Q_AFFINE) return launch_d1x_q<ZMOE_Q_AFFINE>(st, a, d->inter);
   return launch_d1x_q<ZMOE_Q_MXFP4>(st, a, d->inter);
 }

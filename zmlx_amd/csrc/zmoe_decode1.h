@@ -72,6 +72,36 @@ __device__ __forceinline__ int rank_in_row(const uint32_t* keys, int& i, uint32_
   return q == 0 ? cnt : -1;
 }
 
+// Rank of 64-bit key i (number of larger keys; keys are unique) over an
+// EPAD-entry row, Q = 512/EPAD adjacent threads per key, each counting one
+// slice in chunks of up to 16 keys.  Returns the rank in thread q == 0 of each
+// group (-1 elsewhere).
+template <int EPAD>
+__device__ __forceinline__ int rank_in_row64(const uint64_t* keys, int& i, uint64_t& ki) {
+  constexpr int Q = kFThreads / EPAD;
+  constexpr int PER = EPAD / Q;
+  constexpr int CH = PER < 16 ? PER : 16;  // keys per chunk
+  static_assert(Q >= 2 && Q <= 8 && PER % CH == 0 && CH % 2 == 0, "rank slices");
+  i = threadIdx.x / Q;
+  const int q = threadIdx.x % Q;
+  ki = keys[i];
+  int cnt = 0;
+  for (int c = 0; c < PER; c += CH) {
+    uint4 kk[CH / 2];
+#pragma unroll
+    for (int m = 0; m < CH / 2; ++m) kk[m] = *reinterpret_cast<const uint4*>(&keys[q * PER + c + 2 * m]);
+#pragma unroll
+    for (int m = 0; m < CH / 2; ++m) {
+      cnt += ((static_cast<uint64_t>(kk[m].y) << 32 | kk[m].x) > ki) ? 1 : 0;
+      cnt += ((static_cast<uint64_t>(kk[m].w) << 32 | kk[m].z) > ki) ? 1 : 0;
+    }
+  }
+  cnt += __builtin_amdgcn_update_dpp(0, cnt, kDppQuadSwap1, 0xF, 0xF, false);
+  if (Q >= 4) cnt += __builtin_amdgcn_update_dpp(0, cnt, kDppQuadSwap2, 0xF, 0xF, false);
+  if (Q >= 8) cnt += __builtin_amdgcn_update_dpp(0, cnt, kDppHalfMirror, 0xF, 0xF, false);
+  return q == 0 ? cnt : -1;
+}
+
 // Gate weights of the ranked winners (wave 0; lane r < K holds winner r),
 // then the routing outputs of workgroup 0.
 __device__ __forceinline__ void rank_weights(const FusedParams& p, D1Lds& L, int K) {
