@@ -251,6 +251,15 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
       biasv.v[i] = e < E ? gload(p.route.bias + e) : 0.0f;
     }
   }
+  // Grouped sigmoid routers with more than 64 experts score in parallel:
+  // wave w takes experts 64 w .. 64 w + 63 from its own poll (sigmoid, +
+  // bias, its two groups' top-2 sums), then every scoring wave keeps the
+  // same groups and writes its experts' keys -- sig_scores' arithmetic per
+  // expert and per group, spread over E / 64 waves instead of wave 0 alone.
+  const bool par_sig = sig_rank && par_poll;
+  const bool grp_lim = p.route.n_group > 1 && p.route.topk_group < p.route.n_group;
+  float bias_w = 0.0f, sg_w = 0.0f, v_w = 0.0f;
+  if (par_sig && pre_bias && wave * kWave < E) bias_w = gload(p.route.bias + wave * kWave + lane);
   if (par_poll) {
     const int e = wave * kWave + lane;
     if (wave * kWave < E) {
@@ -278,10 +287,38 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
         }
       }
       if (e < E) L.keys[e] = __float_as_uint(round_bf16(a));
+      if (par_sig) {
+        sg_w = sigmoid_abs(round_bf16(a));
+        v_w = sg_w + bias_w;
+        if (grp_lim) {
+          float t1, t2;
+          half_top2(v_w, t1, t2);
+          if ((lane & 31) == 0) L.route.gsc[2 * wave + (lane >> 5)] = t1 + t2;
+        }
+      }
     }
     lds_barrier();
   }
-  if (wave == 0) {
+  if (par_sig) {
+    if (wave * kWave < E) {
+      const int e = wave * kWave + lane;
+      if (grp_lim) {
+        const int ng = p.route.n_group;
+        const uint32_t gk = lane < ng ? order_key(L.route.gsc[lane]) : 0u;
+        int rank = 0;
+        for (int g = 0; g < ng; ++g) {
+          const uint32_t o = order_key(L.route.gsc[g]);
+          rank += (o > gk || (o == gk && g < lane)) ? 1 : 0;
+        }
+        const uint64_t keepm = __ballot(lane < ng && rank < p.route.topk_group);
+        if (!((keepm >> (e >> 5)) & 1ull)) v_w = 0.0f;
+      }
+      reinterpret_cast<uint64_t*>(L.keys)[e] =
+          static_cast<uint64_t>(order_key(v_w)) << 32 | (0xFFFFFFFFu - static_cast<uint32_t>(e));
+      grow[e] = sg_w;
+    }
+    trace_mark(p, 3);
+  } else if (wave == 0) {
     RowVals<P> row;
     if (par_poll) {
 #pragma unroll
