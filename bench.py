@@ -49,7 +49,7 @@ LAYERS = 48
 ROOT = Path(__file__).resolve().parent
 COPY_BYTES = 256 << 20  # calibration copy of --profile-run: reads and writes this many bytes
 # the single-launch kernel of each decode batch (rocprofv3 kernel names)
-DECODE_KERNELS = {1: "zmoe::k_moe_decode1x<0, 2, 768>"}
+DECODE_KERNELS = {1: "zmoe::k_moe_decode1x<0, 2, 768, 1, 8, false>"}
 # committed rocprofv3 counter summaries (profiles/<name>.json) of the decode lines
 COUNTER_FILES = {1: "k_moe_decode1x_qwen3_b1_counters"}
 
