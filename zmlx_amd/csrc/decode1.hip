@@ -181,7 +181,7 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
   // phase A: a contiguous range of (unit, row-group) items
   int a_g0, a_g1, a_cu, a_cr;
   {
-    const int rg_total = Uall * pl.rgu;
+    const int rg_total = (pl.shpre ? K : Uall) * pl.rgu;  // (shpre: the shared unit's rows come earlier)
     a_g0 = min(rg_total, gw * pl.perA);
     a_g1 = min(rg_total, a_g0 + pl.perA);
     a_cu = static_cast<int>(fdiv(static_cast<uint32_t>(a_g0), pl.by_rgu));
@@ -213,6 +213,59 @@ __global__ __launch_bounds__(kFThreads) void k_moe_decode1(FusedParams p) {
   trace_mark(p, 1);
   lds_barrier();
   trace_mark(p, 2);
+
+  // ---------------- S: the shared expert's gate/up rows, before routing ----------------
+  // (general H) The shared expert does not depend on the routing: its
+  // row-groups are dealt to the waves here, while the router partials are
+  // still being exchanged, with phase A's arithmetic (segment steps in order,
+  // the LH-lane sum) and its tagged act stores; phase A then covers the K
+  // routed units only.
+  if constexpr (!XR) {
+    if (pl.shpre) {
+      const int LH = 1 << pl.lLH, RPI = kWave >> pl.lLH;
+      const int rs = lane >> pl.lLH, li = lane & (LH - 1);
+      const int T = pl.TA;
+      const int64_t wpr = H >> 3;
+      const int64_t ppr = (QMODE == ZMOE_Q_AFFINE) ? (S_H >> p.gshift) : S_H;
+      constexpr int SB = 8;  // segment steps per batch of loads
+      for (int g = gw; g < pl.rgu; g += W) {
+        const int64_t row = static_cast<int64_t>(g) * RPI + rs;
+        float ag = 0.0f, au = 0.0f;
+        for (int t0 = 0; t0 < T; t0 += SB) {
+          uint4 wgv[SB], wuv[SB];
+          RawParam rgv[SB], ruv[SB];
+#pragma unroll
+          for (int j = 0; j < SB; ++j) {
+            const int t = min(t0 + j, T - 1);  // past the last step: repeat it (loads stay unconditional)
+            const int sgm = t * LH + li;
+            const int64_t po = row * ppr + ((QMODE == ZMOE_Q_AFFINE) ? (sgm >> p.gshift) : sgm);
+            wgv[j] = gload(reinterpret_cast<const uint4*>(p.w[3] + row * wpr + sgm * 4));
+            wuv[j] = gload(reinterpret_cast<const uint4*>(p.w[4] + row * wpr + sgm * 4));
+            rgv[j] = seg_param_load<QMODE>(p.s[3], p.b[3], po);
+            ruv[j] = seg_param_load<QMODE>(p.s[4], p.b[4], po);
+          }
+#pragma unroll
+          for (int j = 0; j < SB; ++j) {
+            const int t = t0 + j;
+            if (t < T) {
+              const int sgm = t * LH + li;
+              float sgj, cgj, suj, cuj;
+              seg_param_decode<QMODE>(rgv[j], sgj, cgj);
+              seg_param_decode<QMODE>(ruv[j], suj, cuj);
+              const float xsum = (QMODE == ZMOE_Q_AFFINE) ? sx[sgm] : 0.0f;
+              ag = seg_accum<QMODE>(t == 0 ? 0.0f : ag, sgj, cgj, seg_dot_lds<QMODE>(wgv[j], xs, S_H, 0, sgm, ak), xsum);
+              au = seg_accum<QMODE>(t == 0 ? 0.0f : au, suj, cuj, seg_dot_lds<QMODE>(wuv[j], xs, S_H, 0, sgm, ak), xsum);
+            }
+          }
+        }
+        const float gv = lanes_sum(ag, LH);
+        const float uv = lanes_sum(au, LH);
+        if (li == 0)
+          dev_store(p.act + static_cast<int64_t>(K) * p.act_stride + row,
+                    (tag16 << 16) | (wg_dead() ? kBf16NaN : swiglu_bf16(round_bf16(gv), round_bf16(uv))));
+      }
+    }
+  }
 
   // ---------------- T: routing and the unit table ----------------
   // Softmax-probability routers (and top-k over logits with renormalised
@@ -751,6 +804,17 @@ static bool d1_enabled() {
   return on == 1;
 }
 
+// ZMOE_DECODE1_SHARED_EARLY=0: the one-token kernel computes the shared
+// expert's gate/up rows with the routed ones, after the routing.
+static bool d1_shared_early_enabled() {
+  static int on = -1;
+  if (on < 0) {
+    const char* e = getenv("ZMOE_DECODE1_SHARED_EARLY");
+    on = (e && e[0] == '0') ? 0 : 1;
+  }
+  return on == 1;
+}
+
 size_t decode1_lds_bytes(const zmoe_layer_desc* d, int grid) {
   const int Uall = d->top_k + (d->shared_inter > 0 ? 1 : 0);
   const int W = grid * kFWaves;
@@ -813,7 +877,9 @@ int launch_decode1(hipStream_t st, const zmoe_layer_desc* d, const FusedParams& 
   pl.TA = S_H / LH;
   pl.TD = S_I / LI;
   pl.rgu = I / (kWave / LH);
-  pl.perA = (pl.Uall * pl.rgu + W - 1) / W;
+  // the shared expert's gate/up rows before the routing wait (general H)
+  pl.shpre = (d->shared_inter > 0 && !(fp.LH == kWave && fp.H == 32 * kWave) && d1_shared_early_enabled()) ? 1 : 0;
+  pl.perA = ((pl.shpre ? d->top_k : pl.Uall) * pl.rgu + W - 1) / W;
   pl.by_rgu = make_fastdiv(static_cast<uint32_t>(pl.rgu));
   pl.by_Uall = make_fastdiv(static_cast<uint32_t>(pl.Uall));
   pl.by_NC = make_fastdiv(static_cast<uint32_t>(H / 512));

@@ -35,6 +35,7 @@ struct D1Plan {
   int TA, TD;        // segments per lane, phase A / phase D
   int rgu;           // row-groups per unit (phase A)
   int PB;             // act slots per down-projection pass (batched kernel)
+  int shpre;          // one-token kernel, general H: the shared expert's gate/up rows before the routing wait
   FastDiv by_rgu, by_Uall, by_NC, by_W, by_I;
   int64_t wst[3], sst[3];  // per-expert strides: packed words, scale (= bias) bytes
 };
