@@ -361,11 +361,18 @@ static int run_sequence(void* stream, const zmoe_layer_desc* d, const void* x, i
   const void* shared = nullptr;
   if (d->shared_inter > 0) {
     const int Is = d->shared_inter;
+    // From 32 tokens: one "pair" of B token rows (each workgroup reads the
+    // shared weights once for 4 rows; DeepSeek-V3 B=64 1511 -> 1500 us);
+    // smaller batches: B one-row pairs (more workgroups; GLM-shape B=8 71 us
+    // vs 79 us).  The per-token arithmetic is the same either way.
+    const bool rows = B >= 32;
+    const int64_t np = rows ? 1 : B;
+    const int M = rows ? B : 1;
     rc = dispatch_qmv(true, stream, x, d->sh_gate_w, d->sh_gate_s, d->sh_gate_b, d->sh_up_w, d->sh_up_s, d->sh_up_b,
-                      nullptr, nullptr, 1, B, 1, Is, H, d->quant_mode, gshift, ws.sh_act);
+                      nullptr, nullptr, 1, np, M, Is, H, d->quant_mode, gshift, ws.sh_act);
     if (rc) return rc;
     rc = dispatch_qmv(false, stream, ws.sh_act, d->sh_down_w, d->sh_down_s, d->sh_down_b, nullptr, nullptr, nullptr,
-                      nullptr, nullptr, 1, B, 1, H, Is, d->quant_mode, gshift, ws.sh_y);
+                      nullptr, nullptr, 1, np, M, H, Is, d->quant_mode, gshift, ws.sh_y);
     if (rc) return rc;
     shared = ws.sh_y;
   }
