@@ -187,7 +187,7 @@ extern "C" size_t zmoe_moe_layer_trace_info(const zmoe_layer_desc* desc, int B, 
 }
 
 static int run_sequence(void* stream, const zmoe_layer_desc* d, const void* x, int B, void* out, uint32_t* out_idx,
-                        float* out_w, char* ws_base);
+                        float* out_w, char* ws_base, bool side_ok);
 
 extern "C" int zmoe_moe_layer(void* stream, const zmoe_layer_desc* d, const void* x, int B, void* out,
                               uint32_t* out_idx, float* out_w, void* workspace, size_t workspace_bytes) {
@@ -203,13 +203,75 @@ extern "C" int zmoe_moe_layer(void* stream, const zmoe_layer_desc* d, const void
   ZMOE_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, ZMOE_EINVAL_SHAPE,
                "[moe_layer] x must be 16-byte and workspace 256-byte aligned.");
   // multi-kernel sequence: its buffers follow the single-launch kernel's
-  return run_sequence(stream, d, x, B, out, out_idx, out_w, static_cast<char*>(workspace) + multi_ws_offset(d, B));
+  return run_sequence(stream, d, x, B, out, out_idx, out_w, static_cast<char*>(workspace) + multi_ws_offset(d, B),
+                      true);
+}
+
+// The shared expert (a dense SwiGLU MLP on every token): gate/up + SwiGLU,
+// then down, into sh_y.  From 32 tokens as one "pair" of B token rows (each
+// workgroup reads the shared weights once for 4 rows; DeepSeek-V3 B=64 1511
+// -> 1500 us); smaller batches as B one-row pairs (more workgroups; GLM-shape
+// B=8 71 us vs 79 us).  The per-token arithmetic is the same either way.
+static int run_shared(void* stream, const zmoe_layer_desc* d, const void* x, int B, int gshift, void* sh_act,
+                      void* sh_y) {
+  const int H = d->hidden, Is = d->shared_inter;
+  const bool rows = B >= 32;
+  const int64_t np = rows ? 1 : B;
+  const int M = rows ? B : 1;
+  int rc = dispatch_qmv(true, stream, x, d->sh_gate_w, d->sh_gate_s, d->sh_gate_b, d->sh_up_w, d->sh_up_s,
+                        d->sh_up_b, nullptr, nullptr, 1, np, M, Is, H, d->quant_mode, gshift, sh_act);
+  if (rc) return rc;
+  return dispatch_qmv(false, stream, sh_act, d->sh_down_w, d->sh_down_s, d->sh_down_b, nullptr, nullptr, nullptr,
+                      nullptr, nullptr, 1, np, M, H, Is, d->quant_mode, gshift, sh_y);
+}
+
+// A second stream per device for the shared expert of the kernel sequence
+// (created once, default priority), with the fork and join events.
+struct SideStream {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+constexpr int kSideMaxDevices = 64;
+static SideStream g_side[kSideMaxDevices];
+static std::mutex g_side_mu;
+
+static bool side_stream_enabled() {
+  static int on = -1;
+  if (on < 0) {
+    const char* e = getenv("ZMOE_SHARED_STREAM");
+    on = (e && e[0] == '0') ? 0 : 1;
+  }
+  return on == 1;
+}
+
+static int side_stream(SideStream** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  ZMOE_REQUIRE(e == hipSuccess && dev >= 0 && dev < kSideMaxDevices, ZMOE_EHIP, "[moe_layer] hipGetDevice failed.");
+  SideStream& ss = g_side[dev];
+  if (ss.s == nullptr) {
+    hipStream_t s = nullptr;
+    hipEvent_t f = nullptr, j = nullptr;
+    e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&f, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&j, hipEventDisableTiming);
+    ZMOE_REQUIRE(e == hipSuccess, ZMOE_EHIP, std::string("[moe_layer] side stream: ") + hipGetErrorString(e));
+    ss.fork = f;
+    ss.join = j;
+    ss.s = s;
+  }
+  *out = &ss;
+  return ZMOE_OK;
 }
 
 // The multi-kernel sequence over workspace buffers at ws_base (layout_ws);
-// keeps nothing from call to call.
+// keeps nothing from call to call.  With side_ok, a layer's shared expert
+// (it reads only x) runs on a second stream of the library's while the
+// router and the routed experts run on the caller's stream; the combine waits
+// for both (an event fork and join, which a HIP graph capture records as
+// parallel branches).
 static int run_sequence(void* stream, const zmoe_layer_desc* d, const void* x, int B, void* out, uint32_t* out_idx,
-                        float* out_w, char* ws_base) {
+                        float* out_w, char* ws_base, bool side_ok) {
   int rc = ZMOE_OK;
   LayerWs ws = layout_ws(d, B, ws_base);
   ZMOE_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(ws_base) & 255) == 0,
@@ -228,6 +290,27 @@ static int run_sequence(void* stream, const zmoe_layer_desc* d, const void* x, i
   ZMOE_REQUIRE(d->bits == 4, ZMOE_EUNSUPPORTED, "[moe_layer] only 4-bit weights.");
 
   const SeqMode mode = seq_mode(d, B);
+  // 0. the shared expert, on the side stream when allowed
+  const void* shared = nullptr;
+  SideStream* side = nullptr;
+  std::unique_lock<std::mutex> side_lock(g_side_mu, std::defer_lock);
+  if (d->shared_inter > 0) {
+    if (side_ok && side_stream_enabled()) {
+      side_lock.lock();
+      rc = side_stream(&side);
+      if (rc) return rc;
+      hipError_t e = hipEventRecord(side->fork, st);
+      if (e == hipSuccess) e = hipStreamWaitEvent(side->s, side->fork, 0);
+      ZMOE_REQUIRE(e == hipSuccess, ZMOE_EHIP, std::string("[moe_layer] side stream fork: ") + hipGetErrorString(e));
+    }
+    rc = run_shared(side ? static_cast<void*>(side->s) : stream, d, x, B, gshift, ws.sh_act, ws.sh_y);
+    if (rc) return rc;
+    shared = ws.sh_y;
+    if (side) {
+      hipError_t e = hipEventRecord(side->join, side->s);
+      ZMOE_REQUIRE(e == hipSuccess, ZMOE_EHIP, std::string("[moe_layer] side stream join: ") + hipGetErrorString(e));
+    }
+  }
   // 1. router projection (bf16 logits, as the gate nn.Linear returns them)
   // (prefill batches on MFMA; decode batches keep the chunk order that the
   // single-launch kernels reproduce).  At hidden 2048 the MFMA router also
@@ -357,24 +440,11 @@ static int run_sequence(void* stream, const zmoe_layer_desc* d, const void* x, i
                       ws.idx, 1, static_cast<int64_t>(B) * K, 1, H, I, d->quant_mode, gshift, ws.y);
     if (rc) return rc;
   }
-  // 4. shared expert (dense SwiGLU MLP on every token)
-  const void* shared = nullptr;
-  if (d->shared_inter > 0) {
-    const int Is = d->shared_inter;
-    // From 32 tokens: one "pair" of B token rows (each workgroup reads the
-    // shared weights once for 4 rows; DeepSeek-V3 B=64 1511 -> 1500 us);
-    // smaller batches: B one-row pairs (more workgroups; GLM-shape B=8 71 us
-    // vs 79 us).  The per-token arithmetic is the same either way.
-    const bool rows = B >= 32;
-    const int64_t np = rows ? 1 : B;
-    const int M = rows ? B : 1;
-    rc = dispatch_qmv(true, stream, x, d->sh_gate_w, d->sh_gate_s, d->sh_gate_b, d->sh_up_w, d->sh_up_s, d->sh_up_b,
-                      nullptr, nullptr, 1, np, M, Is, H, d->quant_mode, gshift, ws.sh_act);
-    if (rc) return rc;
-    rc = dispatch_qmv(false, stream, ws.sh_act, d->sh_down_w, d->sh_down_s, d->sh_down_b, nullptr, nullptr, nullptr,
-                      nullptr, nullptr, 1, np, M, H, Is, d->quant_mode, gshift, ws.sh_y);
-    if (rc) return rc;
-    shared = ws.sh_y;
+  // 4. the shared expert's result (step 0) is joined before the combine
+  if (side) {
+    const hipError_t e = hipStreamWaitEvent(st, side->join, 0);
+    ZMOE_REQUIRE(e == hipSuccess, ZMOE_EHIP, std::string("[moe_layer] side stream join: ") + hipGetErrorString(e));
+    side_lock.unlock();
   }
   // 5. combine (+ shared) -> bf16
   rc = launch_combine(st, ws.y, ws.w, w_dtype, B, K, H, d->combine_mode, 1, shared, out);
@@ -443,5 +513,5 @@ extern "C" int zmoe_moe_layer_noalloc(void* stream, const zmoe_layer_desc* d, co
   char* base = nullptr;
   rc = scratch_ptr(&base);
   if (rc) return rc;
-  return run_sequence(stream, d, x, B, out, out_idx, out_w, base);
+  return run_sequence(stream, d, x, B, out, out_idx, out_w, base, false);
 }
