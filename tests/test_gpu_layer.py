@@ -345,6 +345,46 @@ def test_single_launch_routing_ties(dev, family, shape, groups):
     assert fused.sync_error() == 0
 
 
+def test_single_launch_softmax_tie_order(dev):
+    """Softmax routing where the bf16 probabilities tie although the logits
+    differ: the ranking (bf16 probability, then lower index) differs from
+    plain logit order; the single-launch kernel's routing and outputs are
+    those of the kernel sequence (bit-identical) and a valid top-k of the
+    oracle's probabilities."""
+    import torch
+
+    from zmlx_amd.layer import QuantizedMoELayer
+
+    rng = np.random.default_rng(29)
+    H, E, I, K = 2048, 128, 768, 8
+    banks, wr, sh, tq, tsh, _ = _build(dev, rng, H=H, E=E, I=I, K=K)
+    # logits = wr[:, 0] for x = e_0: distinct, within 1.3e-2 of each other,
+    # larger for higher indices; probabilities tie in bf16 in runs
+    wr = np.zeros((E, H), np.float32)
+    wr[:, 0] = ((np.arange(E) * 37) % E) * 1e-4
+    wr_t = to_bf16(wr, dev)
+    logits = O.bf16_round(wr[:, 0])
+    probs = O.softmax_precise_bf16(logits)
+    by_logit = np.argsort(-logits, kind="stable")[:K]
+    by_prob = O.topk_desc(probs, K)
+    assert set(by_logit) != set(by_prob)  # logit order would route differently
+    mk = lambda single: QuantizedMoELayer.for_family(  # noqa: E731
+        "qwen3", wr_t, tq["gate"], tq["up"], tq["down"], top_k=K, single_launch=single)
+    fused, multi = mk(True), mk(False)
+    x = np.zeros((1, H), np.float32)
+    x[0, 0] = 1.0
+    xt = to_bf16(x, dev)
+    for rep in range(2):
+        of, i_f, w_f = fused(xt, return_routing=True)
+        om, i_m, w_m = multi(xt, return_routing=True)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(from_dev(i_f), from_dev(i_m))
+        assert O.topk_is_valid(from_dev(i_f)[0], probs, K)
+        np.testing.assert_array_equal(from_dev(w_f), from_dev(w_m))
+        np.testing.assert_array_equal(from_dev(of), from_dev(om))
+    assert fused.sync_error() == 0
+
+
 @pytest.mark.parametrize("mode,gs", [("affine", 64), ("mxfp4", 32)])
 def test_layer_expert_major_gemv(dev, mode, gs):
     """12 tokens over 16 experts (about 3 rows each): the kernel sequence runs
