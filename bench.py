@@ -597,16 +597,18 @@ def main() -> int:
         per_b[str(B)] = rec
         if B == args.batch:
             main_rec = rec
-            # one k_moe_decode launch per layer call: the timed region holds
-            # steps x layers launches and nothing else
-            kname = DECODE_KERNELS.get(B, "zmoe::k_moe_decodeb<0, 2, 4>")
-            tr = (load_profile(COUNTER_FILES.get(B, "")) or {}).get("kernels", {}).get(kname)
+            # B=1: one k_moe_decode1x launch per layer call, so the timed
+            # region holds steps x layers launches and nothing else; other
+            # batches run a kernel sequence, priced per layer call
+            kname = DECODE_KERNELS.get(B)
+            tr = (load_profile(COUNTER_FILES.get(B, "")) or {}).get("kernels", {}).get(kname) if kname else None
             roof = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                     "frac": round(gbps / HBM_PEAK_GBPS, 4),
                     "traffic": int(tr["bytes"]) if tr else None,
-                    "kernel": kname,
-                    "avg_launch_us": round(layer_us, 3),
-                    "alg_bytes_per_launch": int(alg_bytes)}
+                    "kernel": kname or "kernel sequence (k_dense_logits, k_route_rows, k_gather_qmv x2, "
+                                       "k_moe_combine; or k_grouped_qmm from 32 tokens)",
+                    ("avg_launch_us" if kname else "avg_call_us"): round(layer_us, 3),
+                    ("alg_bytes_per_launch" if kname else "alg_bytes_per_call"): int(alg_bytes)}
         log(f"B={B}: {rec}")
 
     if args.prefill > 0:
